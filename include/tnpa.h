@@ -1,0 +1,113 @@
+/* tnpa.h -- C ABI of the MI355X (gfx950) causal polynomial attention library (libtnpa.so).
+ *
+ * The library replaces the Triton host orchestration and kernels of the reference operator
+ * (ref: tnlm/kernels/poly_attn.py). Every entry point takes plain pointers, element strides and sizes; the caller
+ * owns all device memory (the library never allocates), and work is enqueued asynchronously on the caller's HIP
+ * stream (passed as void*, e.g. torch.cuda.current_stream().cuda_stream). Entry points return 0 on success and a
+ * nonzero tnpa_status otherwise; tnpa_last_error() then describes the failure (thread-local). Argument errors are
+ * detected before anything is enqueued.
+ *
+ * Semantics (ref: tnlm/attention.py:22-38,54-77; tnlm/kernels/poly_attn.py:1-16):
+ *   y_i = row_scale_i * sum_{j visible from i} A(S1_ij, S2_ij) v_j,   S_ij = q_i . k_j / sqrt(dk)
+ *   visible(i, j): j <= i, same (contiguous) document, both tokens real (doc id >= 0);
+ *   A: signed_product S1*S2 | offset_square (S1 + b_h)^2 | lower_degree_mix c0 + c1 S1 + c2 S2 + c12 S1 S2
+ *      | power S1^degree (this build's degree-p kind; degree 2 equals signed_product with q2 = q1, k2 = k1).
+ *   The mask is applied after the polynomial; scores, products and accumulators are FP32; the masked product is
+ *   rounded to the input dtype before each matrix-core product.
+ */
+#ifndef TNPA_H
+#define TNPA_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define TNPA_ABI_VERSION 1
+
+typedef enum {
+  TNPA_OK = 0,
+  TNPA_ERR_INVALID = 1,     /* bad shape / stride / dtype / pointer: maps to Python ValueError */
+  TNPA_ERR_UNSUPPORTED = 2, /* valid per the reference contract but outside this build (e.g. head dim 256) */
+  TNPA_ERR_LAUNCH = 3       /* HIP launch failure: maps to Python RuntimeError */
+} tnpa_status;
+
+typedef enum { TNPA_BF16 = 0, TNPA_F32 = 1, TNPA_F16 = 2 } tnpa_dtype;
+
+/* ref: tnlm/kernels/poly_attn.py:23 (KINDS) plus TNPA_POWER */
+typedef enum { TNPA_SIGNED_PRODUCT = 0, TNPA_OFFSET_SQUARE = 1, TNPA_LOWER_DEGREE_MIX = 2, TNPA_POWER = 3 } tnpa_kind;
+
+/* A (B, H, T, d) tensor view: element strides over batch, head and time; the head dim must have unit stride.
+ * Row starts must be 16-byte aligned (data pointer and every stride times the element size). */
+typedef struct {
+  const void* data;
+  int64_t stride_b, stride_h, stride_t;
+} tnpa_tensor_t;
+
+/* Inputs shared by forward and backward. q1/k1/q2/k2 are (B,H,T,dk); v is (B,H,T,dv). For kinds with one pair
+ * (offset_square, power) q2/k2 are ignored. doc_start/query_end come from tnpa_doc_bounds (ref _block_bounds,
+ * tnlm/kernels/poly_attn.py:205-218, restated per token). row_scale is (B,T) fp32 contiguous: n_visible^-p for real
+ * tokens, 0 for padding (ref: tnlm/kernels/poly_attn.py:312-314). coef is (H,4) fp32 contiguous for
+ * lower_degree_mix; offset is (H) fp32 contiguous for offset_square. */
+typedef struct {
+  int32_t batch, heads, seq_len, head_dim_k, head_dim_v;
+  int32_t kind;   /* tnpa_kind */
+  int32_t degree; /* TNPA_POWER only, 1..8 */
+  int32_t dtype;  /* tnpa_dtype of q1, k1, q2, k2, v and of every output / gradient */
+  tnpa_tensor_t q1, k1, q2, k2, v;
+  const int32_t* doc_start;
+  const int32_t* query_end;
+  const float* row_scale;
+  const float* coef;
+  const float* offset;
+} tnpa_problem_t;
+
+/* Gradients for tnpa_backward. dout is dL/dy (B,H,T,dv). dq2/dk2 are ignored for one-pair kinds. dpar_partial is
+ * a caller-allocated fp32 workspace of tnpa_dpar_workspace_floats() floats, and dpar an (H,4) fp32 output
+ * (column 0 = db for offset_square, the 4 columns = dcoef for lower_degree_mix); both may be NULL for
+ * signed_product / power, and are required for the other two kinds. */
+typedef struct {
+  tnpa_tensor_t dout, dq1, dk1, dq2, dk2, dv;
+  float* dpar_partial;
+  float* dpar;
+} tnpa_grads_t;
+
+/* Library ABI version (TNPA_ABI_VERSION). */
+int tnpa_abi_version(void);
+
+/* Message for the last nonzero return on this thread ("" if none). */
+const char* tnpa_last_error(void);
+
+/* Per-token visibility bounds from document ids (B,T), int32 (doc_is_int64 = 0) or int64 (1), row stride
+ * doc_stride_b elements: doc_start[b,t] = first key visible from t (t + 1 for padding), query_end[b,t] = one past
+ * the last query that sees key t. Replaces ref: tnlm/kernels/poly_attn.py:205-218 (_block_bounds) and
+ * ref: tnlm/attention.py:12-19 (doc_positions); ids must be contiguous runs, negative = padding. */
+int tnpa_doc_bounds(const void* doc_ids, int32_t doc_is_int64, int64_t doc_stride_b, int32_t batch,
+                    int32_t seq_len, int32_t* doc_start, int32_t* query_end, void* stream);
+
+/* Forward: writes out (B,H,T,dv) in the problem dtype. Replaces ref: tnlm/kernels/poly_attn.py:271-280
+ * (PolyAttention.forward launch of _fwd). */
+int tnpa_forward(const tnpa_problem_t* problem, const tnpa_tensor_t* out, void* stream);
+
+/* Floats of dpar_partial workspace tnpa_backward needs for this problem (0 for signed_product / power). */
+int64_t tnpa_dpar_workspace_floats(const tnpa_problem_t* problem);
+
+/* Backward: writes dq1, dk1, (dq2, dk2), dv, and dpar. Replaces ref: tnlm/kernels/poly_attn.py:286-309
+ * (PolyAttention.backward: _bwd_kv, _bwd_q and the fixed-order dcoef/db reduction). Deterministic: no atomics,
+ * every reduction in a fixed order. */
+int tnpa_backward(const tnpa_problem_t* problem, const tnpa_grads_t* grads, void* stream);
+
+/* The two passes of tnpa_backward, selectable: TNPA_PHASE_KV writes dk1, (dk2), dv and dpar (ref _bwd_kv,
+ * tnlm/kernels/poly_attn.py:298-299,304-306); TNPA_PHASE_Q writes dq1, (dq2) (ref _bwd_q, :302-303). The passes
+ * read only inputs, so they may run on different streams concurrently. Gradients a phase does not write may be
+ * left NULL. tnpa_backward(...) == tnpa_backward_phase(..., TNPA_PHASE_KV | TNPA_PHASE_Q, ...). */
+#define TNPA_PHASE_KV 1
+#define TNPA_PHASE_Q 2
+int tnpa_backward_phase(const tnpa_problem_t* problem, const tnpa_grads_t* grads, int32_t phases, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* TNPA_H */

@@ -1,0 +1,7 @@
+"""MI355X-native causal polynomial attention (gfx950 HIP kernels behind a C ABI), a drop-in for the Triton
+operator of tnlm (ref: tnlm/kernels/poly_attn.py)."""
+from .config import ATTENTION_BACKENDS, poly_attention_for, resolve_attention_backend  # noqa: F401
+from .poly_attn import KINDS, PolyAttention, doc_bounds, poly_attention_hip  # noqa: F401
+
+__all__ = ["KINDS", "PolyAttention", "poly_attention_hip", "doc_bounds", "ATTENTION_BACKENDS",
+           "resolve_attention_backend", "poly_attention_for"]

@@ -1,0 +1,310 @@
+// C ABI of libtnpa.so: argument validation, dtype/kind/head-dim dispatch to the kernel instantiations, the
+// document-bounds prepass and the fixed-order dcoef/db reduction.  Declared in include/tnpa.h.
+#include <cmath>
+#include <cstdarg>
+#include <cstdio>
+#include <string>
+
+#include "../../include/tnpa.h"
+#include "tnpa_params.hpp"
+
+namespace {
+
+thread_local std::string g_err;
+
+int fail(int code, const char* fmt, ...) {
+  char buf[512];
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(buf, sizeof(buf), fmt, ap);
+  va_end(ap);
+  g_err = buf;
+  return code;
+}
+
+int ok() {
+  g_err.clear();
+  return TNPA_OK;
+}
+
+int esize(int dtype) { return dtype == TNPA_F32 ? 4 : 2; }
+
+bool valid_dim(int d) { return d >= 16 && (d & (d - 1)) == 0; }
+
+// Validates one (B,H,T,d) tensor view. `name` is used in messages.
+int check_tensor(const tnpa_tensor_t& t, const char* name, const tnpa_problem_t& p, int es) {
+  if (t.data == nullptr) return fail(TNPA_ERR_INVALID, "%s: null data pointer", name);
+  if (((uintptr_t)t.data) % 16 != 0) return fail(TNPA_ERR_INVALID, "%s: data pointer not 16-byte aligned", name);
+  if (t.stride_t <= 0 || (t.stride_t * es) % 16 != 0)
+    return fail(TNPA_ERR_INVALID, "%s: time stride %lld elements must be positive with 16-byte aligned rows", name,
+                (long long)t.stride_t);
+  if (p.batch > 1 && (t.stride_b * es) % 16 != 0)
+    return fail(TNPA_ERR_INVALID, "%s: batch stride %lld not 16-byte aligned", name, (long long)t.stride_b);
+  if (p.heads > 1 && (t.stride_h * es) % 16 != 0)
+    return fail(TNPA_ERR_INVALID, "%s: head stride %lld not 16-byte aligned", name, (long long)t.stride_h);
+  return TNPA_OK;
+}
+
+bool two_pairs(int kind) { return kind == TNPA_SIGNED_PRODUCT || kind == TNPA_LOWER_DEGREE_MIX; }
+
+int check_problem(const tnpa_problem_t* pp) {
+  if (pp == nullptr) return fail(TNPA_ERR_INVALID, "null problem");
+  const tnpa_problem_t& p = *pp;
+  if (p.batch <= 0 || p.heads <= 0 || p.seq_len <= 0)
+    return fail(TNPA_ERR_INVALID, "batch, heads and seq_len must be positive (got %d, %d, %d)", p.batch, p.heads,
+                p.seq_len);
+  if (!valid_dim(p.head_dim_k) || !valid_dim(p.head_dim_v))
+    return fail(TNPA_ERR_INVALID, "head dims: powers of 2 >= 16 (got dk=%d, dv=%d)", p.head_dim_k, p.head_dim_v);
+  if (p.head_dim_k > 128 || p.head_dim_v > 128)
+    return fail(TNPA_ERR_UNSUPPORTED, "head dims above 128 are not built (got dk=%d, dv=%d)", p.head_dim_k,
+                p.head_dim_v);
+  if (p.kind < 0 || p.kind > 3) return fail(TNPA_ERR_INVALID, "unknown kind %d", p.kind);
+  if (p.kind == TNPA_POWER && (p.degree < 1 || p.degree > 8))
+    return fail(TNPA_ERR_INVALID, "power kind needs degree in 1..8 (got %d)", p.degree);
+  if (p.dtype != TNPA_BF16 && p.dtype != TNPA_F32 && p.dtype != TNPA_F16)
+    return fail(TNPA_ERR_INVALID, "unknown dtype %d", p.dtype);
+  const long long blocks = (long long)p.batch * p.heads * ((p.seq_len + 31) / 32);
+  if (blocks > 0x7fffffffLL) return fail(TNPA_ERR_UNSUPPORTED, "problem too large for one launch");
+  const int es = esize(p.dtype);
+  int rc;
+  if ((rc = check_tensor(p.q1, "q1", p, es))) return rc;
+  if ((rc = check_tensor(p.k1, "k1", p, es))) return rc;
+  if (two_pairs(p.kind)) {
+    if ((rc = check_tensor(p.q2, "q2", p, es))) return rc;
+    if ((rc = check_tensor(p.k2, "k2", p, es))) return rc;
+  }
+  if ((rc = check_tensor(p.v, "v", p, es))) return rc;
+  if (p.doc_start == nullptr || p.query_end == nullptr)
+    return fail(TNPA_ERR_INVALID, "doc_start / query_end missing (run tnpa_doc_bounds first)");
+  if (p.row_scale == nullptr) return fail(TNPA_ERR_INVALID, "row_scale missing");
+  if (p.kind == TNPA_LOWER_DEGREE_MIX && p.coef == nullptr)
+    return fail(TNPA_ERR_INVALID, "lower_degree_mix needs coef (H,4)");
+  if (p.kind == TNPA_OFFSET_SQUARE && p.offset == nullptr)
+    return fail(TNPA_ERR_INVALID, "offset_square needs offset (H)");
+  return TNPA_OK;
+}
+
+tnpa::TDesc desc(const tnpa_tensor_t& t) { return tnpa::TDesc{t.data, t.stride_b, t.stride_h, t.stride_t}; }
+
+tnpa::KParams make_params(const tnpa_problem_t& p) {
+  tnpa::KParams k{};
+  k.q1 = desc(p.q1);
+  k.k1 = desc(p.k1);
+  k.q2 = two_pairs(p.kind) ? desc(p.q2) : desc(p.q1);
+  k.k2 = two_pairs(p.kind) ? desc(p.k2) : desc(p.k1);
+  k.v = desc(p.v);
+  k.dstart = p.doc_start;
+  k.qend = p.query_end;
+  k.rscale = p.row_scale;
+  k.coef = p.coef;
+  k.offs = p.offset;
+  k.B = p.batch;
+  k.H = p.heads;
+  k.T = p.seq_len;
+  k.kind = p.kind;
+  k.deg = p.kind == TNPA_POWER ? p.degree : 2;
+  const double sm = 1.0 / std::sqrt((double)p.head_dim_k);
+  k.sm = (float)sm;
+  switch (p.kind) {
+    case TNPA_SIGNED_PRODUCT: k.vf = (float)(sm * sm); k.gf = (float)(sm * sm); break;
+    case TNPA_POWER: k.vf = (float)std::pow(sm, k.deg); k.gf = (float)(k.deg * std::pow(sm, k.deg)); break;
+    default: k.vf = 1.0f; k.gf = (float)sm; break;
+  }
+  return k;
+}
+
+int poly_of(const tnpa_problem_t& p) {
+  if (p.kind == TNPA_POWER) return p.degree == 2 ? tnpa::POLY_POW2 : tnpa::POLY_GEN1;
+  if (p.kind == TNPA_OFFSET_SQUARE) return tnpa::POLY_GEN1;
+  return tnpa::POLY_GEN2;
+}
+
+enum Phase { PH_FWD = 0, PH_BWD_KV = 1, PH_BWD_Q = 2 };
+
+template <typename T, int POLY>
+hipError_t run_dims(int ph, int dk, int dv, const tnpa::KParams& k, hipStream_t s) {
+#define TNPA_CASE(DK_, DV_)                                                                   \
+  if (dk == DK_ && dv == DV_)                                                                 \
+    return ph == PH_FWD      ? tnpa::launch_fwd<T, POLY, DK_, DV_>(k, s)                      \
+           : ph == PH_BWD_KV ? tnpa::launch_bwd_kv<T, POLY, DK_, DV_>(k, s)                   \
+                             : tnpa::launch_bwd_q<T, POLY, DK_, DV_>(k, s);
+#define TNPA_ROW(DK_) TNPA_CASE(DK_, 16) TNPA_CASE(DK_, 32) TNPA_CASE(DK_, 64) TNPA_CASE(DK_, 128)
+  TNPA_ROW(16) TNPA_ROW(32) TNPA_ROW(64) TNPA_ROW(128)
+#undef TNPA_ROW
+#undef TNPA_CASE
+  return hipErrorInvalidValue;
+}
+
+template <typename T>
+hipError_t run_poly(int ph, int poly, int dk, int dv, const tnpa::KParams& k, hipStream_t s) {
+  switch (poly) {
+    case tnpa::POLY_GEN1: return run_dims<T, tnpa::POLY_GEN1>(ph, dk, dv, k, s);
+    case tnpa::POLY_GEN2: return run_dims<T, tnpa::POLY_GEN2>(ph, dk, dv, k, s);
+    default: return run_dims<T, tnpa::POLY_POW2>(ph, dk, dv, k, s);
+  }
+}
+
+hipError_t run(int ph, const tnpa_problem_t& p, const tnpa::KParams& k, hipStream_t s) {
+  const int poly = poly_of(p);
+  switch (p.dtype) {
+    case TNPA_BF16: return run_poly<__bf16>(ph, poly, p.head_dim_k, p.head_dim_v, k, s);
+    case TNPA_F16: return run_poly<_Float16>(ph, poly, p.head_dim_k, p.head_dim_v, k, s);
+    default: return run_poly<float>(ph, poly, p.head_dim_k, p.head_dim_v, k, s);
+  }
+}
+
+// ---------------------------------------------------------------------------------------------- prepass kernels
+// One workgroup per batch row. doc_start[t] = start of t's run (t + 1 for padding) via a max-scan of run starts;
+// query_end[t] = next run start after t (t for padding) via a reverse min-scan.
+__global__ void __launch_bounds__(256) k_doc_bounds(const void* doc, int is64, int64_t sb, int T, int* dstart,
+                                                    int* qend) {
+  constexpr int NT = 256;
+  const int b = blockIdx.x, t = threadIdx.x;
+  const int L = (T + NT - 1) / NT;
+  const int s0 = min(t * L, T), s1 = min(s0 + L, T);
+  const int64_t* d64 = (const int64_t*)doc + (int64_t)b * sb;
+  const int* d32 = (const int*)doc + (int64_t)b * sb;
+  auto id = [&](int i) -> int64_t { return is64 ? d64[i] : (int64_t)d32[i]; };
+  auto is_start = [&](int i) -> bool { return i == 0 || id(i) != id(i - 1); };
+  int last = -1, first = T;
+  for (int i = s0; i < s1; ++i)
+    if (is_start(i)) {
+      last = i;
+      if (first == T) first = i;
+    }
+  __shared__ int sl[NT], sf[NT];
+  sl[t] = last;
+  sf[t] = first;
+  __syncthreads();
+  for (int off = 1; off < NT; off <<= 1) {
+    const int a = t >= off ? sl[t - off] : -1;
+    const int c = t + off < NT ? sf[t + off] : T;
+    __syncthreads();
+    sl[t] = max(sl[t], a);
+    sf[t] = min(sf[t], c);
+    __syncthreads();
+  }
+  int cur = t > 0 ? sl[t - 1] : -1;
+  int nxt = t < NT - 1 ? sf[t + 1] : T;
+  int* ds = dstart + (int64_t)b * T;
+  int* qe = qend + (int64_t)b * T;
+  for (int i = s0; i < s1; ++i) {
+    if (is_start(i)) cur = i;
+    ds[i] = id(i) < 0 ? i + 1 : cur;
+  }
+  for (int i = s1 - 1; i >= s0; --i) {
+    qe[i] = id(i) < 0 ? i : nxt;
+    if (is_start(i)) nxt = i;
+  }
+}
+
+// dpar[h, c] = sum over (b, key block) of the per-block partials, in a fixed order.
+// ref: tnlm/kernels/poly_attn.py:304 (dpar.view(B, H, NB, 4).sum((0, 2)))
+__global__ void k_dpar_reduce(const float* part, int B, int H, int NNB, float* out) {
+  const int i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= H * 4) return;
+  const int hd = i / 4, c = i % 4;
+  float acc = 0.f;
+  for (int b = 0; b < B; ++b)
+    for (int nb = 0; nb < NNB; ++nb) acc += part[(((int64_t)b * H + hd) * NNB + nb) * 4 + c];
+  out[i] = acc;
+}
+
+}  // namespace
+
+extern "C" {
+
+int tnpa_abi_version(void) { return TNPA_ABI_VERSION; }
+
+const char* tnpa_last_error(void) { return g_err.c_str(); }
+
+int tnpa_doc_bounds(const void* doc_ids, int32_t doc_is_int64, int64_t doc_stride_b, int32_t batch, int32_t seq_len,
+                    int32_t* doc_start, int32_t* query_end, void* stream) {
+  if (doc_ids == nullptr || doc_start == nullptr || query_end == nullptr)
+    return fail(TNPA_ERR_INVALID, "tnpa_doc_bounds: null pointer");
+  if (batch <= 0 || seq_len <= 0) return fail(TNPA_ERR_INVALID, "tnpa_doc_bounds: batch and seq_len must be positive");
+  if (batch > 1 && doc_stride_b < seq_len)
+    return fail(TNPA_ERR_INVALID, "tnpa_doc_bounds: batch stride %lld shorter than seq_len", (long long)doc_stride_b);
+  hipLaunchKernelGGL(k_doc_bounds, dim3(batch), dim3(256), 0, (hipStream_t)stream, doc_ids, doc_is_int64 ? 1 : 0,
+                     doc_stride_b, seq_len, doc_start, query_end);
+  const hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return fail(TNPA_ERR_LAUNCH, "tnpa_doc_bounds: %s", hipGetErrorString(e));
+  return ok();
+}
+
+int tnpa_forward(const tnpa_problem_t* problem, const tnpa_tensor_t* out, void* stream) {
+  int rc = check_problem(problem);
+  if (rc) return rc;
+  if (out == nullptr) return fail(TNPA_ERR_INVALID, "null out");
+  if ((rc = check_tensor(*out, "out", *problem, esize(problem->dtype)))) return rc;
+  tnpa::KParams k = make_params(*problem);
+  k.o = desc(*out);
+  const hipError_t e = run(PH_FWD, *problem, k, (hipStream_t)stream);
+  if (e != hipSuccess) return fail(TNPA_ERR_LAUNCH, "tnpa_forward: %s", hipGetErrorString(e));
+  return ok();
+}
+
+int64_t tnpa_dpar_workspace_floats(const tnpa_problem_t* problem) {
+  if (problem == nullptr) return 0;
+  if (problem->kind != TNPA_OFFSET_SQUARE && problem->kind != TNPA_LOWER_DEGREE_MIX) return 0;
+  const int64_t nnb = (problem->seq_len + tnpa::KV_BLOCK_KEYS - 1) / tnpa::KV_BLOCK_KEYS;
+  return (int64_t)problem->batch * problem->heads * nnb * 4;
+}
+
+int tnpa_backward_phase(const tnpa_problem_t* problem, const tnpa_grads_t* grads, int32_t phases, void* stream) {
+  int rc = check_problem(problem);
+  if (rc) return rc;
+  if (grads == nullptr) return fail(TNPA_ERR_INVALID, "null grads");
+  if (phases <= 0 || phases > (TNPA_PHASE_KV | TNPA_PHASE_Q))
+    return fail(TNPA_ERR_INVALID, "phases must be a nonzero combination of TNPA_PHASE_KV and TNPA_PHASE_Q");
+  const tnpa_problem_t& p = *problem;
+  const int es = esize(p.dtype);
+  const bool kv = phases & TNPA_PHASE_KV, q = phases & TNPA_PHASE_Q;
+  if ((rc = check_tensor(grads->dout, "dout", p, es))) return rc;
+  if (q && (rc = check_tensor(grads->dq1, "dq1", p, es))) return rc;
+  if (kv && (rc = check_tensor(grads->dk1, "dk1", p, es))) return rc;
+  if (kv && (rc = check_tensor(grads->dv, "dv", p, es))) return rc;
+  if (two_pairs(p.kind)) {
+    if (q && (rc = check_tensor(grads->dq2, "dq2", p, es))) return rc;
+    if (kv && (rc = check_tensor(grads->dk2, "dk2", p, es))) return rc;
+  }
+  const bool par = kv && (p.kind == TNPA_OFFSET_SQUARE || p.kind == TNPA_LOWER_DEGREE_MIX);
+  if (par && (grads->dpar_partial == nullptr || grads->dpar == nullptr))
+    return fail(TNPA_ERR_INVALID, "offset_square / lower_degree_mix need dpar_partial and dpar");
+  tnpa::KParams k = make_params(p);
+  k.dout = desc(grads->dout);
+  if (q) {
+    k.dq1 = desc(grads->dq1);
+    k.dq2 = two_pairs(p.kind) ? desc(grads->dq2) : desc(grads->dq1);
+  }
+  if (kv) {
+    k.dk1 = desc(grads->dk1);
+    k.dk2 = two_pairs(p.kind) ? desc(grads->dk2) : desc(grads->dk1);
+    k.dv = desc(grads->dv);
+  }
+  k.dpar = par ? grads->dpar_partial : nullptr;
+  hipError_t e;
+  if (kv) {
+    e = run(PH_BWD_KV, p, k, (hipStream_t)stream);
+    if (e != hipSuccess) return fail(TNPA_ERR_LAUNCH, "tnpa_backward (dK/dV): %s", hipGetErrorString(e));
+  }
+  if (q) {
+    e = run(PH_BWD_Q, p, k, (hipStream_t)stream);
+    if (e != hipSuccess) return fail(TNPA_ERR_LAUNCH, "tnpa_backward (dQ): %s", hipGetErrorString(e));
+  }
+  if (par) {
+    const int nnb = (p.seq_len + tnpa::KV_BLOCK_KEYS - 1) / tnpa::KV_BLOCK_KEYS;
+    const int n = p.heads * 4;
+    hipLaunchKernelGGL(k_dpar_reduce, dim3((n + 255) / 256), dim3(256), 0, (hipStream_t)stream, grads->dpar_partial,
+                       p.batch, p.heads, nnb, grads->dpar);
+    e = hipGetLastError();
+    if (e != hipSuccess) return fail(TNPA_ERR_LAUNCH, "tnpa_backward (dpar): %s", hipGetErrorString(e));
+  }
+  return ok();
+}
+
+int tnpa_backward(const tnpa_problem_t* problem, const tnpa_grads_t* grads, void* stream) {
+  return tnpa_backward_phase(problem, grads, TNPA_PHASE_KV | TNPA_PHASE_Q, stream);
+}
+
+}  // extern "C"

@@ -1,0 +1,232 @@
+// Device primitives for the CDNA4 (gfx950) causal polynomial attention kernels.
+//
+// Everything here is written for 64-wide wavefronts and the gfx950 MFMA units:
+//   * bf16/fp16 inputs use v_mfma_f32_32x32x16_{bf16,f16}: per lane an 8-element A and B operand, 16 fp32
+//     accumulators; fp32 inputs use v_mfma_f32_32x32x2_f32 (one element per lane).
+//   * 32x32 accumulator layout (probed on the MI355X): register r of lane l holds row
+//     8*(r/4) + 4*(l/32) + r%4, column l%32. Operand layout: lane l supplies row/column l%32 and the K elements
+//     EPL*(l/32) .. EPL*(l/32)+EPL-1 of each KC-wide chunk.
+//   * An accumulator is reused as the next MFMA's operand without any shuffle: the rows of the tile that is read
+//     as the A operand are permuted by `kappa` so that accumulator register r of lane-half h holds K index
+//     key_off(r, h) = (r/EPL)*KC + h*EPL + r%EPL, which is exactly the natural operand order.
+//   * Operands whose contraction runs along the tile rows are read with ds_read_b64_tr_b16 (gfx950 LDS transpose
+//     read): inside each 16-lane group, lanes 4r..4r+3 each supply 4 consecutive elements of row r and lane i
+//     receives element i of rows 0..3.
+//   * LDS tiles are row-major with a 16-byte-chunk XOR swizzle so that both the row-wise 128-bit reads and the
+//     transposed 64-bit reads avoid bank conflicts.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#define TNPA_LDS __attribute__((address_space(3)))
+
+namespace tnpa {
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef short s16x4 __attribute__((ext_vector_type(4)));
+typedef short s16x8 __attribute__((ext_vector_type(8)));
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+
+// ------------------------------------------------------------------------------------------------ MFMA traits
+template <typename T> struct Mfma;
+
+template <> struct Mfma<__bf16> {
+  static constexpr int KC = 16;  // contraction length of one MFMA
+  static constexpr int EPL = 8;  // operand elements per lane
+  typedef bf16x8 Op;
+  __device__ static inline f32x16 mma(Op a, Op b, f32x16 c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
+  }
+  __device__ static inline Op cvt(const float* f) {
+    Op o;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) o[j] = (__bf16)f[j];
+    return o;
+  }
+  __device__ static inline Op zero() {
+    Op o;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) o[j] = (__bf16)0.0f;
+    return o;
+  }
+};
+
+template <> struct Mfma<_Float16> {
+  static constexpr int KC = 16;
+  static constexpr int EPL = 8;
+  typedef f16x8 Op;
+  __device__ static inline f32x16 mma(Op a, Op b, f32x16 c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
+  }
+  __device__ static inline Op cvt(const float* f) {
+    Op o;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) o[j] = (_Float16)f[j];
+    return o;
+  }
+  __device__ static inline Op zero() {
+    Op o;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) o[j] = (_Float16)0.0f;
+    return o;
+  }
+};
+
+template <> struct Mfma<float> {
+  static constexpr int KC = 2;
+  static constexpr int EPL = 1;
+  typedef float Op;
+  __device__ static inline f32x16 mma(Op a, Op b, f32x16 c) {
+    return __builtin_amdgcn_mfma_f32_32x32x2f32(a, b, c, 0, 0, 0);
+  }
+  __device__ static inline Op cvt(const float* f) { return f[0]; }
+  __device__ static inline Op zero() { return 0.0f; }
+};
+
+__device__ inline f32x16 zero16() {
+  f32x16 z;
+#pragma unroll
+  for (int i = 0; i < 16; ++i) z[i] = 0.0f;
+  return z;
+}
+
+// K index held by accumulator register r of lane-half h once the A-operand rows were read through kappa().
+template <typename T> __device__ constexpr inline int key_off(int r, int h) {
+  return (r / Mfma<T>::EPL) * Mfma<T>::KC + h * Mfma<T>::EPL + r % Mfma<T>::EPL;
+}
+// Tile row that lane (l % 32) = i must supply as the A operand so that register r / half h holds key_off(r, h).
+template <typename T> __device__ constexpr inline int kappa(int i) {
+  return key_off<T>(4 * (i / 8) + i % 4, (i / 4) % 2);
+}
+
+// ------------------------------------------------------------------------------------------------ LDS tiles
+// Row-major ROWS x WID tile of T, WID a multiple of 32 (head dims below 32 are zero padded). Stored in 16-byte
+// chunks with chunk index XOR-swizzled by row.
+template <typename T, int ROWS, int WID> struct Tile {
+  static constexpr int CE = 16 / (int)sizeof(T);  // elements per 16-byte chunk
+  static constexpr int NCH = WID / CE;            // chunks per row
+  static constexpr int BYTES = ROWS * WID * (int)sizeof(T);
+  static_assert(NCH >= 4 && (NCH & (NCH - 1)) == 0, "tile width");
+  __device__ static inline int swz(int r) {
+    if constexpr (NCH >= 16) return ((r & 3) << 2) | ((r >> 2) & 3);
+    else if constexpr (NCH == 8) return (((r >> 1) & 1) << 2) | ((r >> 2) & 3);
+    else return (r >> 2) & 3;
+  }
+  // byte offset of element (r, col)
+  __device__ static inline uint32_t off(int r, int col) {
+    const int ch = col / CE, e = col % CE;
+    return (uint32_t)(((r * NCH + (ch ^ swz(r))) * 16) + e * (int)sizeof(T));
+  }
+};
+
+// A/B operand whose contraction runs along the row (head dim): elements [c*KC + h*EPL, +EPL) of tile row `row`.
+template <typename T, typename TL>
+__device__ inline typename Mfma<T>::Op read_row(const char TNPA_LDS* tile, int row, int c, int h) {
+  typedef typename Mfma<T>::Op Op;
+  const int col = c * Mfma<T>::KC + h * Mfma<T>::EPL;
+  return *(const Op TNPA_LDS*)(tile + TL::off(row, col));
+}
+
+// A/B operand whose contraction runs down the rows: lane (n = l%32, h) gets tile[k0 + h*EPL + j][col0 + n].
+template <typename T, typename TL>
+__device__ inline typename Mfma<T>::Op read_col(const char TNPA_LDS* tile, int k0, int col0, int lane) {
+  typedef typename Mfma<T>::Op Op;
+  if constexpr (sizeof(T) == 2) {
+    const int i = lane & 15, g = lane >> 4, hh = lane >> 5;
+    const int col = col0 + 16 * (g & 1) + 4 * (i & 3);
+    const int row = k0 + 8 * hh + (i >> 2);
+    s16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((s16x4 TNPA_LDS*)(tile + TL::off(row, col)));
+    s16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((s16x4 TNPA_LDS*)(tile + TL::off(row + 4, col)));
+    s16x8 both = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
+    return __builtin_bit_cast(Op, both);
+  } else {
+    return *(const float TNPA_LDS*)(tile + TL::off(k0 + (lane >> 5), col0 + (lane & 31)));
+  }
+}
+
+// Operand loaded straight from global memory (kept in registers for the whole kernel): row-major global row
+// pointer, elements [c*KC + h*EPL, +EPL).
+template <typename T>
+__device__ inline typename Mfma<T>::Op load_op(const T* __restrict__ rowp, int c, int h) {
+  typedef typename Mfma<T>::Op Op;
+  return *(const Op*)(rowp + c * Mfma<T>::KC + h * Mfma<T>::EPL);
+}
+
+// ------------------------------------------------------------------------------------------------ staging
+// Global -> registers -> LDS copy of a ROWS x D tile (D real columns of a WID-wide LDS tile), 16 bytes per
+// access; consecutive threads take consecutive chunks of a row (coalesced). Rows at or past `nvalid` read as
+// zero. Optionally scales each row by a per-row factor (used to fold the row scale into dO).
+template <typename T, int ROWS, int D, int WID, int NT> struct Stage {
+  static constexpr int CE = 16 / (int)sizeof(T);
+  static constexpr int NCHG = D / CE;
+  static constexpr int TOTAL = ROWS * NCHG;
+  static constexpr int PER = (TOTAL + NT - 1) / NT;
+  typedef Tile<T, ROWS, WID> TL;
+  u32x4 r[PER];
+
+  __device__ inline void load(const T* __restrict__ g, int64_t st, int row0, int nvalid) {
+#pragma unroll
+    for (int i = 0; i < PER; ++i) {
+      const int idx = (int)threadIdx.x + i * NT;
+      r[i] = u32x4{0u, 0u, 0u, 0u};
+      if (TOTAL % NT == 0 || idx < TOTAL) {
+        const int rr = idx / NCHG, c = idx % NCHG;
+        if (rr < nvalid) r[i] = *(const u32x4*)(g + (int64_t)(row0 + rr) * st + c * CE);
+      }
+    }
+  }
+  // same, scaling row rr by scale[row0 + rr]
+  __device__ inline void load_scaled(const T* __restrict__ g, int64_t st, int row0, int nvalid,
+                                     const float* __restrict__ scale) {
+#pragma unroll
+    for (int i = 0; i < PER; ++i) {
+      const int idx = (int)threadIdx.x + i * NT;
+      r[i] = u32x4{0u, 0u, 0u, 0u};
+      if (TOTAL % NT == 0 || idx < TOTAL) {
+        const int rr = idx / NCHG, c = idx % NCHG;
+        if (rr < nvalid) {
+          u32x4 raw = *(const u32x4*)(g + (int64_t)(row0 + rr) * st + c * CE);
+          const float f = scale[row0 + rr];
+          if constexpr (sizeof(T) == 2) {
+            T* e = reinterpret_cast<T*>(&raw);
+#pragma unroll
+            for (int j = 0; j < 8; ++j) e[j] = (T)((float)e[j] * f);
+          } else {
+            float* e = reinterpret_cast<float*>(&raw);
+#pragma unroll
+            for (int j = 0; j < 4; ++j) e[j] *= f;
+          }
+          r[i] = raw;
+        }
+      }
+    }
+  }
+  __device__ inline void store(char TNPA_LDS* tile) const {
+#pragma unroll
+    for (int i = 0; i < PER; ++i) {
+      const int idx = (int)threadIdx.x + i * NT;
+      if (TOTAL % NT == 0 || idx < TOTAL) {
+        const int rr = idx / NCHG, c = idx % NCHG;
+        *(u32x4 TNPA_LDS*)(tile + TL::off(rr, c * CE)) = r[i];
+      }
+    }
+  }
+};
+
+// Stores 4 consecutive output elements (one accumulator register group) converted to T.
+template <typename T> __device__ inline void store4(T* __restrict__ p, float a, float b, float c, float d) {
+  if constexpr (sizeof(T) == 2) {
+    typedef T T4 __attribute__((ext_vector_type(4)));
+    T4 v;
+    v[0] = (T)a; v[1] = (T)b; v[2] = (T)c; v[3] = (T)d;
+    *(T4*)p = v;
+  } else {
+    *(f32x4*)p = f32x4{a, b, c, d};
+  }
+}
+
+}  // namespace tnpa

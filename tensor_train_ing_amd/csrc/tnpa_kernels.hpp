@@ -1,0 +1,748 @@
+// Causal polynomial attention kernels for gfx950: forward, dQ and dK/dV.
+//
+// Operator semantics follow ref: tnlm/kernels/poly_attn.py:1-16 and the dense reference
+// ref: tnlm/attention.py:22-38,54-77:
+//     y_i = scale_i * sum_{j visible from i} A(S1_ij, S2_ij) v_j,   S_ij = q_i . k_j / sqrt(dk),
+// visible(i, j) <=> doc_start[i] <= j <= i (contiguous documents; padding rows see nothing), the mask applied
+// after the polynomial, FP32 accumulation, the masked product cast to the input dtype before each MFMA.
+//
+// Work decomposition (one workgroup = NW wavefronts of 64 lanes):
+//   forward, dQ:  a workgroup owns BM = NW*QW*32 queries; wave w owns QW 32-query subtiles whose Q (and dO)
+//                 operands stay in registers; K/V tiles of BN keys are staged through double-buffered LDS.
+//                 S^T = K Q^T and dP^T = V dO^T leave lane <-> query, so P^T/dS^T feed O^T += V^T P^T and
+//                 dQ^T += K^T dS^T directly as B operands (V^T, K^T read with the LDS transpose read).
+//   dK/dV:        a workgroup owns NW*KW*32 keys; K/V operands stay in registers; Q/dO tiles of BMQ queries are
+//                 staged through LDS (dO pre-multiplied by the row scale while staging). S = Q K^T and
+//                 dP = dO V^T leave lane <-> key, so P/dS feed dV^T += dO^T P and dK^T += Q^T dS.
+// Causal skipping: the key/query loop bounds stop at the diagonal and at document starts (tile level), and each
+// wave skips 32x32 sub-blocks that are fully invisible to it (wavefront level). Only sub-blocks that straddle the
+// diagonal, a document edge or the sequence end evaluate the per-element mask.
+// Work items are ordered heaviest first (longest causal range), and consecutive items cycle through (b, h) so
+// that all blocks of one head land on the same XCD (blockIdx % 8) and share its L2.
+#pragma once
+
+#include <climits>
+
+#include "tnpa_device.hpp"
+#include "tnpa_params.hpp"
+
+namespace tnpa {
+
+struct Coefs {
+  float c0, c1, c2, c12;
+};
+
+__device__ inline Coefs load_coefs(const KParams& p, int hd) {
+  Coefs c{0.f, 0.f, 0.f, 0.f};
+  if (p.kind == KIND_LDM && p.coef) {
+    c.c0 = p.coef[hd * 4 + 0]; c.c1 = p.coef[hd * 4 + 1]; c.c2 = p.coef[hd * 4 + 2]; c.c12 = p.coef[hd * 4 + 3];
+  } else if (p.kind == KIND_OS && p.offs) {
+    c.c0 = p.offs[hd];
+  }
+  return c;
+}
+
+// A(S1, S2) on raw dot products r = q.k (homogeneous kinds fold sm^p into vf).  ref: tnlm/kernels/poly_attn.py:26-34
+template <int POLY>
+__device__ inline float poly_value(float r1, float r2, int kind, int deg, float sm, const Coefs& c) {
+  if constexpr (POLY == POLY_POW2) {
+    return r1 * r1;
+  } else if constexpr (POLY == POLY_GEN1) {
+    if (kind == KIND_OS) {
+      const float t = fmaf(r1, sm, c.c0);
+      return t * t;
+    }
+    float v = r1;
+    for (int i = 1; i < deg; ++i) v *= r1;
+    return v;
+  } else {
+    if (kind == KIND_SP) return r1 * r2;
+    const float s1 = r1 * sm, s2 = r2 * sm;
+    return c.c0 + c.c1 * s1 + c.c2 * s2 + c.c12 * s1 * s2;
+  }
+}
+
+// dS1, dS2 for a masked upstream H entry hg (gf carries the constant factors); optionally accumulates the
+// head-scalar partial sums g[0..3].  ref: tnlm/kernels/poly_attn.py:123-135,189-196
+template <int POLY, bool PAR>
+__device__ inline void poly_grad(float r1, float r2, float hg, int kind, int deg, float sm, const Coefs& c,
+                                 float& d1, float& d2, float* g) {
+  if constexpr (POLY == POLY_POW2) {
+    d1 = hg * r1;
+    d2 = 0.f;
+  } else if constexpr (POLY == POLY_GEN1) {
+    d2 = 0.f;
+    if (kind == KIND_OS) {
+      d1 = 2.0f * hg * fmaf(r1, sm, c.c0);
+      if constexpr (PAR) g[0] += d1;
+    } else {
+      float v = 1.0f;
+      for (int i = 1; i < deg; ++i) v *= r1;
+      d1 = hg * v;
+    }
+  } else {
+    if (kind == KIND_SP) {
+      d1 = hg * r2;
+      d2 = hg * r1;
+    } else {
+      const float s1 = r1 * sm, s2 = r2 * sm;
+      d1 = hg * (c.c1 + c.c12 * s2);
+      d2 = hg * (c.c2 + c.c12 * s1);
+      if constexpr (PAR) {
+        g[0] += hg; g[1] += hg * s1; g[2] += hg * s2; g[3] += hg * s1 * s2;
+      }
+    }
+  }
+}
+
+template <typename T> __device__ inline const T* head_ptr(const TDesc& d, int b, int hd) {
+  return (const T*)d.p + (int64_t)b * d.sb + (int64_t)hd * d.sh;
+}
+template <typename T> __device__ inline T* head_ptr_w(const TDesc& d, int b, int hd) {
+  return (T*)d.p + (int64_t)b * d.sb + (int64_t)hd * d.sh;
+}
+
+// ------------------------------------------------------------------------------------------------ tile configs
+template <typename T, int POLY, int DK, int DV> struct Cfg {
+  static constexpr bool F32 = sizeof(T) == 4;
+  static constexpr int NPAIR = POLY == POLY_GEN2 ? 2 : 1;
+  static constexpr int FW_NW = 4, FW_QW = F32 ? 1 : 2, FW_BN = F32 ? 32 : 64;
+  static constexpr int BQ_NW = 4, BQ_QW = (F32 || NPAIR == 2) ? 1 : 2, BQ_BN = F32 ? 32 : 64;
+  static constexpr int KV_NW = 4, KV_KW = 1, KV_BM = F32 ? 32 : 64;
+  static constexpr int KV_KEYS = KV_NW * KV_KW * 32;
+};
+
+// ------------------------------------------------------------------------------------------------ forward
+// ref: tnlm/kernels/poly_attn.py:37-74 (_fwd)
+template <typename T, int POLY, int DK, int DV, int NW, int QW, int BN>
+__global__ void __launch_bounds__(NW * 64) k_fwd(const KParams p) {
+  typedef Mfma<T> M;
+  typedef typename M::Op Op;
+  constexpr int KC = M::KC, EPL = M::EPL, NT = NW * 64;
+  constexpr int NPAIR = POLY == POLY_GEN2 ? 2 : 1;
+  constexpr int DKP = DK < 32 ? 32 : DK, DVP = DV < 32 ? 32 : DV;
+  constexpr int NCK = DK / KC, NDV = DVP / 32, NKB = BN / 32, NC2 = 32 / KC;
+  constexpr int BM = NW * QW * 32;
+  typedef Tile<T, BN, DKP> KTile;
+  typedef Tile<T, BN, DVP> VTile;
+  constexpr int BUF = NPAIR * KTile::BYTES + VTile::BYTES;
+  __shared__ __attribute__((aligned(16))) char smem_[2 * BUF];
+  char TNPA_LDS* smem = (char TNPA_LDS*)smem_;
+
+  const int T_ = p.T, BH = p.B * p.H;
+  const int NMB = (T_ + BM - 1) / BM;
+  const int item = blockIdx.x;
+  const int mb = NMB - 1 - item / BH, bh = item % BH, b = bh / p.H, hd = bh % p.H;
+  const int m0 = mb * BM;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, h = lane >> 5, l32 = lane & 31;
+
+  const T* qp[2] = {head_ptr<T>(p.q1, b, hd), head_ptr<T>(p.q2, b, hd)};
+  const T* kp[2] = {head_ptr<T>(p.k1, b, hd), head_ptr<T>(p.k2, b, hd)};
+  const int64_t qst[2] = {p.q1.st, p.q2.st}, kst[2] = {p.k1.st, p.k2.st};
+  const T* vp = head_ptr<T>(p.v, b, hd);
+  const Coefs cf = load_coefs(p, hd);
+  const int* dst = p.dstart + (int64_t)b * T_;
+  const float* rsc = p.rscale + (int64_t)b * T_;
+
+  if constexpr (DKP != DK || DVP != DV) {
+    for (int i = threadIdx.x; i < 2 * BUF / 16; i += NT) ((u32x4 TNPA_LDS*)smem)[i] = u32x4{0u, 0u, 0u, 0u};
+    __syncthreads();
+  }
+
+  const int qw0 = m0 + wave * QW * 32;
+  Op qf[NPAIR][QW][NCK];
+  int dsq[QW], qa[QW], ql[QW], dsa[QW], dsl[QW];
+  float scq[QW];
+#pragma unroll
+  for (int s = 0; s < QW; ++s) {
+    qa[s] = qw0 + 32 * s;
+    ql[s] = min(qa[s] + 31, T_ - 1);
+    dsa[s] = qa[s] < T_ ? dst[qa[s]] : INT_MAX;
+    dsl[s] = qa[s] < T_ ? dst[ql[s]] : INT_MAX;
+    const int q = qa[s] + l32;
+    const bool valid = q < T_;
+    dsq[s] = valid ? dst[q] : INT_MAX;
+    scq[s] = valid ? rsc[q] : 0.f;
+#pragma unroll
+    for (int pr = 0; pr < NPAIR; ++pr)
+#pragma unroll
+      for (int c = 0; c < NCK; ++c) qf[pr][s][c] = valid ? load_op<T>(qp[pr] + (int64_t)q * qst[pr], c, h) : M::zero();
+  }
+
+  f32x16 oacc[QW][NDV];
+#pragma unroll
+  for (int s = 0; s < QW; ++s)
+#pragma unroll
+    for (int d = 0; d < NDV; ++d) oacc[s][d] = zero16();
+
+  const int lo = (dst[m0] / BN) * BN;
+  const int hi = min(m0 + BM, T_);
+  Stage<T, BN, DK, DKP, NT> sk[NPAIR];
+  Stage<T, BN, DV, DVP, NT> sv;
+#pragma unroll
+  for (int pr = 0; pr < NPAIR; ++pr) sk[pr].load(kp[pr], kst[pr], lo, T_ - lo);
+  sv.load(vp, p.v.st, lo, T_ - lo);
+#pragma unroll
+  for (int pr = 0; pr < NPAIR; ++pr) sk[pr].store(smem + pr * KTile::BYTES);
+  sv.store(smem + NPAIR * KTile::BYTES);
+  __syncthreads();
+
+  int cur = 0;
+  for (int n0 = lo; n0 < hi; n0 += BN) {
+    const bool more = n0 + BN < hi;
+    if (more) {
+#pragma unroll
+      for (int pr = 0; pr < NPAIR; ++pr) sk[pr].load(kp[pr], kst[pr], n0 + BN, T_ - n0 - BN);
+      sv.load(vp, p.v.st, n0 + BN, T_ - n0 - BN);
+    }
+    const char TNPA_LDS* base = smem + cur * BUF;
+#pragma unroll
+    for (int kb = 0; kb < NKB; ++kb) {
+      const int key0 = n0 + 32 * kb;
+      bool act[QW];
+      bool any = false;
+#pragma unroll
+      for (int s = 0; s < QW; ++s) {
+        act[s] = qa[s] < T_ && key0 <= ql[s] && key0 + 31 >= dsa[s];
+        any |= act[s];
+      }
+      if (!any) continue;
+      f32x16 sacc[NPAIR][QW];
+#pragma unroll
+      for (int pr = 0; pr < NPAIR; ++pr)
+#pragma unroll
+        for (int s = 0; s < QW; ++s) sacc[pr][s] = zero16();
+      const int krow = 32 * kb + kappa<T>(l32);
+#pragma unroll
+      for (int c = 0; c < NCK; ++c)
+#pragma unroll
+        for (int pr = 0; pr < NPAIR; ++pr) {
+          const Op a = read_row<T, KTile>(base + pr * KTile::BYTES, krow, c, h);
+#pragma unroll
+          for (int s = 0; s < QW; ++s)
+            if (act[s]) sacc[pr][s] = M::mma(a, qf[pr][s][c], sacc[pr][s]);
+        }
+      Op pop[QW][NC2];
+#pragma unroll
+      for (int s = 0; s < QW; ++s) {
+        if (!act[s]) continue;
+        const bool full = key0 + 31 <= qa[s] && dsl[s] <= key0;
+        const int q = qa[s] + l32;
+        float pv[16];
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          float val = poly_value<POLY>(sacc[0][s][r], sacc[NPAIR - 1][s][r], p.kind, p.deg, p.sm, cf);
+          if (!full) {
+            const int key = key0 + key_off<T>(r, h);
+            if (key > q || key < dsq[s]) val = 0.f;
+          }
+          pv[r] = val;
+        }
+#pragma unroll
+        for (int c2 = 0; c2 < NC2; ++c2) pop[s][c2] = M::cvt(pv + c2 * EPL);
+      }
+#pragma unroll
+      for (int d = 0; d < NDV; ++d)
+#pragma unroll
+        for (int c2 = 0; c2 < NC2; ++c2) {
+          const Op a = read_col<T, VTile>(base + NPAIR * KTile::BYTES, 32 * kb + c2 * KC, 32 * d, lane);
+#pragma unroll
+          for (int s = 0; s < QW; ++s)
+            if (act[s]) oacc[s][d] = M::mma(a, pop[s][c2], oacc[s][d]);
+        }
+    }
+    if (more) {
+      char TNPA_LDS* nxt = smem + (cur ^ 1) * BUF;
+#pragma unroll
+      for (int pr = 0; pr < NPAIR; ++pr) sk[pr].store(nxt + pr * KTile::BYTES);
+      sv.store(nxt + NPAIR * KTile::BYTES);
+    }
+    __syncthreads();
+    cur ^= 1;
+  }
+
+  T* op = head_ptr_w<T>(p.o, b, hd);
+#pragma unroll
+  for (int s = 0; s < QW; ++s) {
+    const int q = qa[s] + l32;
+    if (q >= T_) continue;
+    const float f = scq[s] * p.vf;
+    T* row = op + (int64_t)q * p.o.st;
+#pragma unroll
+    for (int d = 0; d < NDV; ++d)
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        const int col = 32 * d + 8 * g + 4 * h;
+        if (col < DV)
+          store4<T>(row + col, oacc[s][d][4 * g] * f, oacc[s][d][4 * g + 1] * f, oacc[s][d][4 * g + 2] * f,
+                    oacc[s][d][4 * g + 3] * f);
+      }
+  }
+}
+
+// ------------------------------------------------------------------------------------------------ dQ
+// ref: tnlm/kernels/poly_attn.py:151-202 (_bwd_q)
+template <typename T, int POLY, int DK, int DV, int NW, int QW, int BN>
+__global__ void __launch_bounds__(NW * 64) k_bwd_q(const KParams p) {
+  typedef Mfma<T> M;
+  typedef typename M::Op Op;
+  constexpr int KC = M::KC, EPL = M::EPL, NT = NW * 64;
+  constexpr int NPAIR = POLY == POLY_GEN2 ? 2 : 1;
+  constexpr int DKP = DK < 32 ? 32 : DK, DVP = DV < 32 ? 32 : DV;
+  constexpr int NCK = DK / KC, NCV = DV / KC, NDK = DKP / 32, NKB = BN / 32, NC2 = 32 / KC;
+  constexpr int BM = NW * QW * 32;
+  typedef Tile<T, BN, DKP> KTile;
+  typedef Tile<T, BN, DVP> VTile;
+  constexpr int BUF = NPAIR * KTile::BYTES + VTile::BYTES;
+  __shared__ __attribute__((aligned(16))) char smem_[2 * BUF];
+  char TNPA_LDS* smem = (char TNPA_LDS*)smem_;
+
+  const int T_ = p.T, BH = p.B * p.H;
+  const int NMB = (T_ + BM - 1) / BM;
+  const int item = blockIdx.x;
+  const int mb = NMB - 1 - item / BH, bh = item % BH, b = bh / p.H, hd = bh % p.H;
+  const int m0 = mb * BM;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, h = lane >> 5, l32 = lane & 31;
+
+  const T* qp[2] = {head_ptr<T>(p.q1, b, hd), head_ptr<T>(p.q2, b, hd)};
+  const T* kp[2] = {head_ptr<T>(p.k1, b, hd), head_ptr<T>(p.k2, b, hd)};
+  const int64_t qst[2] = {p.q1.st, p.q2.st}, kst[2] = {p.k1.st, p.k2.st};
+  const T* vp = head_ptr<T>(p.v, b, hd);
+  const T* dop = head_ptr<T>(p.dout, b, hd);
+  const Coefs cf = load_coefs(p, hd);
+  const int* dst = p.dstart + (int64_t)b * T_;
+  const float* rsc = p.rscale + (int64_t)b * T_;
+
+  if constexpr (DKP != DK || DVP != DV) {
+    for (int i = threadIdx.x; i < 2 * BUF / 16; i += NT) ((u32x4 TNPA_LDS*)smem)[i] = u32x4{0u, 0u, 0u, 0u};
+    __syncthreads();
+  }
+
+  const int qw0 = m0 + wave * QW * 32;
+  Op qf[NPAIR][QW][NCK];
+  Op dof[QW][NCV];
+  int dsq[QW], qa[QW], ql[QW], dsa[QW], dsl[QW];
+  float scq[QW];
+#pragma unroll
+  for (int s = 0; s < QW; ++s) {
+    qa[s] = qw0 + 32 * s;
+    ql[s] = min(qa[s] + 31, T_ - 1);
+    dsa[s] = qa[s] < T_ ? dst[qa[s]] : INT_MAX;
+    dsl[s] = qa[s] < T_ ? dst[ql[s]] : INT_MAX;
+    const int q = qa[s] + l32;
+    const bool valid = q < T_;
+    dsq[s] = valid ? dst[q] : INT_MAX;
+    scq[s] = valid ? rsc[q] : 0.f;
+#pragma unroll
+    for (int pr = 0; pr < NPAIR; ++pr)
+#pragma unroll
+      for (int c = 0; c < NCK; ++c) qf[pr][s][c] = valid ? load_op<T>(qp[pr] + (int64_t)q * qst[pr], c, h) : M::zero();
+#pragma unroll
+    for (int c = 0; c < NCV; ++c) dof[s][c] = valid ? load_op<T>(dop + (int64_t)q * p.dout.st, c, h) : M::zero();
+  }
+
+  f32x16 dq[NPAIR][QW][NDK];
+#pragma unroll
+  for (int pr = 0; pr < NPAIR; ++pr)
+#pragma unroll
+    for (int s = 0; s < QW; ++s)
+#pragma unroll
+      for (int d = 0; d < NDK; ++d) dq[pr][s][d] = zero16();
+
+  const int lo = (dst[m0] / BN) * BN;
+  const int hi = min(m0 + BM, T_);
+  Stage<T, BN, DK, DKP, NT> sk[NPAIR];
+  Stage<T, BN, DV, DVP, NT> sv;
+#pragma unroll
+  for (int pr = 0; pr < NPAIR; ++pr) sk[pr].load(kp[pr], kst[pr], lo, T_ - lo);
+  sv.load(vp, p.v.st, lo, T_ - lo);
+#pragma unroll
+  for (int pr = 0; pr < NPAIR; ++pr) sk[pr].store(smem + pr * KTile::BYTES);
+  sv.store(smem + NPAIR * KTile::BYTES);
+  __syncthreads();
+
+  int cur = 0;
+  for (int n0 = lo; n0 < hi; n0 += BN) {
+    const bool more = n0 + BN < hi;
+    if (more) {
+#pragma unroll
+      for (int pr = 0; pr < NPAIR; ++pr) sk[pr].load(kp[pr], kst[pr], n0 + BN, T_ - n0 - BN);
+      sv.load(vp, p.v.st, n0 + BN, T_ - n0 - BN);
+    }
+    const char TNPA_LDS* base = smem + cur * BUF;
+#pragma unroll
+    for (int kb = 0; kb < NKB; ++kb) {
+      const int key0 = n0 + 32 * kb;
+      bool act[QW];
+      bool any = false;
+#pragma unroll
+      for (int s = 0; s < QW; ++s) {
+        act[s] = qa[s] < T_ && key0 <= ql[s] && key0 + 31 >= dsa[s];
+        any |= act[s];
+      }
+      if (!any) continue;
+      f32x16 sacc[NPAIR][QW], pacc[QW];
+#pragma unroll
+      for (int s = 0; s < QW; ++s) {
+        pacc[s] = zero16();
+#pragma unroll
+        for (int pr = 0; pr < NPAIR; ++pr) sacc[pr][s] = zero16();
+      }
+      const int krow = 32 * kb + kappa<T>(l32);
+#pragma unroll
+      for (int c = 0; c < NCK; ++c)
+#pragma unroll
+        for (int pr = 0; pr < NPAIR; ++pr) {
+          const Op a = read_row<T, KTile>(base + pr * KTile::BYTES, krow, c, h);
+#pragma unroll
+          for (int s = 0; s < QW; ++s)
+            if (act[s]) sacc[pr][s] = M::mma(a, qf[pr][s][c], sacc[pr][s]);
+        }
+#pragma unroll
+      for (int c = 0; c < NCV; ++c) {
+        const Op a = read_row<T, VTile>(base + NPAIR * KTile::BYTES, krow, c, h);
+#pragma unroll
+        for (int s = 0; s < QW; ++s)
+          if (act[s]) pacc[s] = M::mma(a, dof[s][c], pacc[s]);
+      }
+      Op dso[NPAIR][QW][NC2];
+#pragma unroll
+      for (int s = 0; s < QW; ++s) {
+        if (!act[s]) continue;
+        const bool full = key0 + 31 <= qa[s] && dsl[s] <= key0;
+        const int q = qa[s] + l32;
+        float d1[16], d2[16];
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          float hg = pacc[s][r];
+          if (!full) {
+            const int key = key0 + key_off<T>(r, h);
+            if (key > q || key < dsq[s]) hg = 0.f;
+          }
+          poly_grad<POLY, false>(sacc[0][s][r], sacc[NPAIR - 1][s][r], hg, p.kind, p.deg, p.sm, cf, d1[r], d2[r],
+                                 nullptr);
+        }
+#pragma unroll
+        for (int c2 = 0; c2 < NC2; ++c2) {
+          dso[0][s][c2] = M::cvt(d1 + c2 * EPL);
+          if constexpr (NPAIR == 2) dso[NPAIR - 1][s][c2] = M::cvt(d2 + c2 * EPL);
+        }
+      }
+#pragma unroll
+      for (int pr = 0; pr < NPAIR; ++pr)
+#pragma unroll
+        for (int d = 0; d < NDK; ++d)
+#pragma unroll
+          for (int c2 = 0; c2 < NC2; ++c2) {
+            const Op a = read_col<T, KTile>(base + pr * KTile::BYTES, 32 * kb + c2 * KC, 32 * d, lane);
+#pragma unroll
+            for (int s = 0; s < QW; ++s)
+              if (act[s]) dq[pr][s][d] = M::mma(a, dso[pr][s][c2], dq[pr][s][d]);
+          }
+    }
+    if (more) {
+      char TNPA_LDS* nxt = smem + (cur ^ 1) * BUF;
+#pragma unroll
+      for (int pr = 0; pr < NPAIR; ++pr) sk[pr].store(nxt + pr * KTile::BYTES);
+      sv.store(nxt + NPAIR * KTile::BYTES);
+    }
+    __syncthreads();
+    cur ^= 1;
+  }
+
+  const TDesc* outs[2] = {&p.dq1, &p.dq2};
+#pragma unroll
+  for (int pr = 0; pr < NPAIR; ++pr) {
+    T* dqp = head_ptr_w<T>(*outs[pr], b, hd);
+#pragma unroll
+    for (int s = 0; s < QW; ++s) {
+      const int q = qa[s] + l32;
+      if (q >= T_) continue;
+      const float f = scq[s] * p.gf;
+      T* row = dqp + (int64_t)q * outs[pr]->st;
+#pragma unroll
+      for (int d = 0; d < NDK; ++d)
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+          const int col = 32 * d + 8 * g + 4 * h;
+          if (col < DK)
+            store4<T>(row + col, dq[pr][s][d][4 * g] * f, dq[pr][s][d][4 * g + 1] * f, dq[pr][s][d][4 * g + 2] * f,
+                      dq[pr][s][d][4 * g + 3] * f);
+        }
+    }
+  }
+}
+
+// ------------------------------------------------------------------------------------------------ dK / dV
+// ref: tnlm/kernels/poly_attn.py:77-148 (_bwd_kv)
+template <typename T, int POLY, int DK, int DV, int NW, int KW, int BMQ>
+__global__ void __launch_bounds__(NW * 64) k_bwd_kv(const KParams p) {
+  typedef Mfma<T> M;
+  typedef typename M::Op Op;
+  constexpr int KC = M::KC, EPL = M::EPL, NT = NW * 64;
+  constexpr int NPAIR = POLY == POLY_GEN2 ? 2 : 1;
+  constexpr bool PAR = POLY != POLY_POW2;
+  constexpr int DKP = DK < 32 ? 32 : DK, DVP = DV < 32 ? 32 : DV;
+  constexpr int NCK = DK / KC, NCV = DV / KC, NDK = DKP / 32, NDV = DVP / 32, NQB = BMQ / 32, NC2 = 32 / KC;
+  constexpr int BNK = NW * KW * 32;
+  typedef Tile<T, BMQ, DKP> QTile;
+  typedef Tile<T, BMQ, DVP> OTile;
+  constexpr int BUF = NPAIR * QTile::BYTES + OTile::BYTES + BMQ * 4;
+  __shared__ __attribute__((aligned(16))) char smem_[2 * BUF];
+  __shared__ float red_[NW][4];
+  char TNPA_LDS* smem = (char TNPA_LDS*)smem_;
+
+  const int T_ = p.T, BH = p.B * p.H;
+  const int NNB = (T_ + BNK - 1) / BNK;
+  const int item = blockIdx.x;
+  const int nb = item / BH, bh = item % BH, b = bh / p.H, hd = bh % p.H;
+  const int n0 = nb * BNK;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, h = lane >> 5, l32 = lane & 31;
+
+  const T* qp[2] = {head_ptr<T>(p.q1, b, hd), head_ptr<T>(p.q2, b, hd)};
+  const T* kp[2] = {head_ptr<T>(p.k1, b, hd), head_ptr<T>(p.k2, b, hd)};
+  const int64_t qst[2] = {p.q1.st, p.q2.st}, kst[2] = {p.k1.st, p.k2.st};
+  const T* vp = head_ptr<T>(p.v, b, hd);
+  const T* dop = head_ptr<T>(p.dout, b, hd);
+  const Coefs cf = load_coefs(p, hd);
+  const int* dst = p.dstart + (int64_t)b * T_;
+  const float* rsc = p.rscale + (int64_t)b * T_;
+
+  if constexpr (DKP != DK || DVP != DV) {
+    for (int i = threadIdx.x; i < 2 * BUF / 16; i += NT) ((u32x4 TNPA_LDS*)smem)[i] = u32x4{0u, 0u, 0u, 0u};
+    __syncthreads();
+  }
+
+  const int nw0 = n0 + wave * KW * 32;
+  Op kf[NPAIR][KW][NCK];
+  Op vf[KW][NCV];
+  int ka[KW];
+#pragma unroll
+  for (int s = 0; s < KW; ++s) {
+    ka[s] = nw0 + 32 * s;
+    const int key = ka[s] + l32;
+    const bool valid = key < T_;
+#pragma unroll
+    for (int pr = 0; pr < NPAIR; ++pr)
+#pragma unroll
+      for (int c = 0; c < NCK; ++c) kf[pr][s][c] = valid ? load_op<T>(kp[pr] + (int64_t)key * kst[pr], c, h) : M::zero();
+#pragma unroll
+    for (int c = 0; c < NCV; ++c) vf[s][c] = valid ? load_op<T>(vp + (int64_t)key * p.v.st, c, h) : M::zero();
+  }
+
+  f32x16 dk[NPAIR][KW][NDK], dv[KW][NDV];
+#pragma unroll
+  for (int s = 0; s < KW; ++s) {
+#pragma unroll
+    for (int d = 0; d < NDV; ++d) dv[s][d] = zero16();
+#pragma unroll
+    for (int pr = 0; pr < NPAIR; ++pr)
+#pragma unroll
+      for (int d = 0; d < NDK; ++d) dk[pr][s][d] = zero16();
+  }
+  float gsum[4] = {0.f, 0.f, 0.f, 0.f};
+
+  const int qlo = (n0 / BMQ) * BMQ;
+  const int qhi = p.qend[(int64_t)b * T_ + min(n0 + BNK, T_) - 1];
+  Stage<T, BMQ, DK, DKP, NT> sq[NPAIR];
+  Stage<T, BMQ, DV, DVP, NT> so;
+  constexpr int DSOFF = NPAIR * QTile::BYTES + OTile::BYTES;
+#pragma unroll
+  for (int pr = 0; pr < NPAIR; ++pr) sq[pr].load(qp[pr], qst[pr], qlo, T_ - qlo);
+  so.load_scaled(dop, p.dout.st, qlo, T_ - qlo, rsc);
+  int dsv = 0;
+  if (threadIdx.x < BMQ) dsv = qlo + (int)threadIdx.x < T_ ? dst[qlo + threadIdx.x] : INT_MAX;
+#pragma unroll
+  for (int pr = 0; pr < NPAIR; ++pr) sq[pr].store(smem + pr * QTile::BYTES);
+  so.store(smem + NPAIR * QTile::BYTES);
+  if (threadIdx.x < BMQ) ((int TNPA_LDS*)(smem + DSOFF))[threadIdx.x] = dsv;
+  __syncthreads();
+
+  int cur = 0;
+  for (int m = qlo; m < qhi; m += BMQ) {
+    const bool more = m + BMQ < qhi;
+    if (more) {
+#pragma unroll
+      for (int pr = 0; pr < NPAIR; ++pr) sq[pr].load(qp[pr], qst[pr], m + BMQ, T_ - m - BMQ);
+      so.load_scaled(dop, p.dout.st, m + BMQ, T_ - m - BMQ, rsc);
+      if (threadIdx.x < BMQ) dsv = m + BMQ + (int)threadIdx.x < T_ ? dst[m + BMQ + threadIdx.x] : INT_MAX;
+    }
+    const char TNPA_LDS* base = smem + cur * BUF;
+    const int TNPA_LDS* dsl = (const int TNPA_LDS*)(base + DSOFF);
+#pragma unroll
+    for (int qb = 0; qb < NQB; ++qb) {
+      const int q0 = m + 32 * qb;
+      if (q0 >= T_) continue;
+      const int qlast = min(q0 + 31, T_ - 1);
+      const int ds0 = dsl[32 * qb], dsL = dsl[qlast - m];
+      bool act[KW];
+      bool any = false;
+#pragma unroll
+      for (int s = 0; s < KW; ++s) {
+        act[s] = ka[s] < T_ && ka[s] <= qlast && ka[s] + 31 >= ds0;
+        any |= act[s];
+      }
+      if (!any) continue;
+      f32x16 sacc[NPAIR][KW], pacc[KW];
+#pragma unroll
+      for (int s = 0; s < KW; ++s) {
+        pacc[s] = zero16();
+#pragma unroll
+        for (int pr = 0; pr < NPAIR; ++pr) sacc[pr][s] = zero16();
+      }
+      const int qrow = 32 * qb + kappa<T>(l32);
+#pragma unroll
+      for (int c = 0; c < NCK; ++c)
+#pragma unroll
+        for (int pr = 0; pr < NPAIR; ++pr) {
+          const Op a = read_row<T, QTile>(base + pr * QTile::BYTES, qrow, c, h);
+#pragma unroll
+          for (int s = 0; s < KW; ++s)
+            if (act[s]) sacc[pr][s] = M::mma(a, kf[pr][s][c], sacc[pr][s]);
+        }
+#pragma unroll
+      for (int c = 0; c < NCV; ++c) {
+        const Op a = read_row<T, OTile>(base + NPAIR * QTile::BYTES, qrow, c, h);
+#pragma unroll
+        for (int s = 0; s < KW; ++s)
+          if (act[s]) pacc[s] = M::mma(a, vf[s][c], pacc[s]);
+      }
+      Op po[KW][NC2];
+      Op dso[NPAIR][KW][NC2];
+#pragma unroll
+      for (int s = 0; s < KW; ++s) {
+        if (!act[s]) continue;
+        const bool full = ka[s] + 31 <= q0 && dsL <= ka[s] && q0 + 31 < T_;
+        const int key = ka[s] + l32;
+        float pv[16], d1[16], d2[16];
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int qo = 32 * qb + key_off<T>(r, h);
+          bool vis = true;
+          if (!full) vis = key <= m + qo && dsl[qo] <= key;
+          const float r1 = sacc[0][s][r], r2 = sacc[NPAIR - 1][s][r];
+          pv[r] = vis ? poly_value<POLY>(r1, r2, p.kind, p.deg, p.sm, cf) : 0.f;
+          const float hg = vis ? pacc[s][r] : 0.f;
+          poly_grad<POLY, PAR>(r1, r2, hg, p.kind, p.deg, p.sm, cf, d1[r], d2[r], gsum);
+        }
+#pragma unroll
+        for (int c2 = 0; c2 < NC2; ++c2) {
+          po[s][c2] = M::cvt(pv + c2 * EPL);
+          dso[0][s][c2] = M::cvt(d1 + c2 * EPL);
+          if constexpr (NPAIR == 2) dso[NPAIR - 1][s][c2] = M::cvt(d2 + c2 * EPL);
+        }
+      }
+#pragma unroll
+      for (int d = 0; d < NDV; ++d)
+#pragma unroll
+        for (int c2 = 0; c2 < NC2; ++c2) {
+          const Op a = read_col<T, OTile>(base + NPAIR * QTile::BYTES, 32 * qb + c2 * KC, 32 * d, lane);
+#pragma unroll
+          for (int s = 0; s < KW; ++s)
+            if (act[s]) dv[s][d] = M::mma(a, po[s][c2], dv[s][d]);
+        }
+#pragma unroll
+      for (int pr = 0; pr < NPAIR; ++pr)
+#pragma unroll
+        for (int d = 0; d < NDK; ++d)
+#pragma unroll
+          for (int c2 = 0; c2 < NC2; ++c2) {
+            const Op a = read_col<T, QTile>(base + pr * QTile::BYTES, 32 * qb + c2 * KC, 32 * d, lane);
+#pragma unroll
+            for (int s = 0; s < KW; ++s)
+              if (act[s]) dk[pr][s][d] = M::mma(a, dso[pr][s][c2], dk[pr][s][d]);
+          }
+    }
+    if (more) {
+      char TNPA_LDS* nxt = smem + (cur ^ 1) * BUF;
+#pragma unroll
+      for (int pr = 0; pr < NPAIR; ++pr) sq[pr].store(nxt + pr * QTile::BYTES);
+      so.store(nxt + NPAIR * QTile::BYTES);
+      if (threadIdx.x < BMQ) ((int TNPA_LDS*)(nxt + DSOFF))[threadIdx.x] = dsv;
+    }
+    __syncthreads();
+    cur ^= 1;
+  }
+
+  const TDesc* kouts[2] = {&p.dk1, &p.dk2};
+#pragma unroll
+  for (int s = 0; s < KW; ++s) {
+    const int key = ka[s] + l32;
+    if (key >= T_) continue;
+    T* vrow = head_ptr_w<T>(p.dv, b, hd) + (int64_t)key * p.dv.st;
+#pragma unroll
+    for (int d = 0; d < NDV; ++d)
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        const int col = 32 * d + 8 * g + 4 * h;
+        if (col < DV)
+          store4<T>(vrow + col, dv[s][d][4 * g] * p.vf, dv[s][d][4 * g + 1] * p.vf, dv[s][d][4 * g + 2] * p.vf,
+                    dv[s][d][4 * g + 3] * p.vf);
+      }
+#pragma unroll
+    for (int pr = 0; pr < NPAIR; ++pr) {
+      T* krow = head_ptr_w<T>(*kouts[pr], b, hd) + (int64_t)key * kouts[pr]->st;
+#pragma unroll
+      for (int d = 0; d < NDK; ++d)
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+          const int col = 32 * d + 8 * g + 4 * h;
+          if (col < DK)
+            store4<T>(krow + col, dk[pr][s][d][4 * g] * p.gf, dk[pr][s][d][4 * g + 1] * p.gf,
+                      dk[pr][s][d][4 * g + 2] * p.gf, dk[pr][s][d][4 * g + 3] * p.gf);
+        }
+    }
+  }
+
+  if constexpr (PAR) {
+    if (p.dpar != nullptr && (p.kind == KIND_OS || p.kind == KIND_LDM)) {
+      // fixed-order reduction: lanes (butterfly), then waves in index order
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        float x = gsum[i];
+#pragma unroll
+        for (int o = 32; o >= 1; o >>= 1) x += __shfl_xor(x, o, 64);
+        gsum[i] = x;
+      }
+      if (lane == 0) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) red_[wave][i] = gsum[i];
+      }
+      __syncthreads();
+      if (threadIdx.x < 4) {
+        float acc = 0.f;
+        for (int w = 0; w < NW; ++w) acc += red_[w][threadIdx.x];
+        p.dpar[((int64_t)bh * NNB + nb) * 4 + threadIdx.x] = acc;
+      }
+    }
+  }
+}
+
+// ------------------------------------------------------------------------------------------------ launchers
+template <typename T, int POLY, int DK, int DV> hipError_t launch_fwd(const KParams& p, hipStream_t st) {
+  typedef Cfg<T, POLY, DK, DV> C;
+  constexpr int BM = C::FW_NW * C::FW_QW * 32;
+  const int grid = p.B * p.H * ((p.T + BM - 1) / BM);
+  hipLaunchKernelGGL((k_fwd<T, POLY, DK, DV, C::FW_NW, C::FW_QW, C::FW_BN>), dim3(grid), dim3(C::FW_NW * 64), 0, st, p);
+  return hipGetLastError();
+}
+
+template <typename T, int POLY, int DK, int DV> hipError_t launch_bwd_kv(const KParams& p, hipStream_t st) {
+  typedef Cfg<T, POLY, DK, DV> C;
+  static_assert(C::KV_KEYS == KV_BLOCK_KEYS, "dK/dV block size is fixed");
+  const int grid = p.B * p.H * ((p.T + C::KV_KEYS - 1) / C::KV_KEYS);
+  hipLaunchKernelGGL((k_bwd_kv<T, POLY, DK, DV, C::KV_NW, C::KV_KW, C::KV_BM>), dim3(grid), dim3(C::KV_NW * 64), 0, st,
+                     p);
+  return hipGetLastError();
+}
+
+template <typename T, int POLY, int DK, int DV> hipError_t launch_bwd_q(const KParams& p, hipStream_t st) {
+  typedef Cfg<T, POLY, DK, DV> C;
+  constexpr int BM = C::BQ_NW * C::BQ_QW * 32;
+  const int grid = p.B * p.H * ((p.T + BM - 1) / BM);
+  hipLaunchKernelGGL((k_bwd_q<T, POLY, DK, DV, C::BQ_NW, C::BQ_QW, C::BQ_BN>), dim3(grid), dim3(C::BQ_NW * 64), 0, st,
+                     p);
+  return hipGetLastError();
+}
+
+}  // namespace tnpa

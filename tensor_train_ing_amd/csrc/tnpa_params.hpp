@@ -1,0 +1,42 @@
+// Kernel parameter block and launcher declarations shared by the C-ABI translation unit and the kernel
+// instantiation units (the API unit sees only these declarations, so it compiles no kernel).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace tnpa {
+
+enum Kind { KIND_SP = 0, KIND_OS = 1, KIND_LDM = 2, KIND_POW = 3 };
+// Compile-time polynomial families: GEN1 = one q/k pair (offset_square, power of any degree), GEN2 = two pairs
+// (signed_product, lower_degree_mix), POW2 = power of degree 2 (also signed_product with shared pairs).
+enum Poly { POLY_GEN1 = 0, POLY_GEN2 = 1, POLY_POW2 = 2 };
+
+struct TDesc {
+  const void* p;
+  int64_t sb, sh, st;  // element strides over batch, head, time; unit stride over the head dim
+};
+
+struct KParams {
+  TDesc q1, k1, q2, k2, v, o;
+  TDesc dout, dq1, dk1, dq2, dk2, dv;
+  const int* dstart;   // (B, T) first visible key of each query (q + 1 for padding)
+  const int* qend;     // (B, T) one past the last query that sees each key
+  const float* rscale; // (B, T) row scale n_visible^-p (0 for padding)
+  const float* coef;   // (H, 4) lower_degree_mix coefficients or null
+  const float* offs;   // (H) offset_square offsets or null
+  float* dpar;         // (B*H, NNB, 4) per-key-block partial sums for dcoef / db, or null
+  int B, H, T;
+  int kind, deg;
+  float sm;  // 1/sqrt(dk)
+  float vf;  // factor on forward outputs and dV (sm^p for homogeneous kinds, else 1)
+  float gf;  // factor on dQ and dK (p*sm^p, sm^2 or sm)
+};
+
+constexpr int KV_BLOCK_KEYS = 128;  // keys per dK/dV workgroup for every configuration (sizes the dpar workspace)
+
+template <typename T, int POLY, int DK, int DV> hipError_t launch_fwd(const KParams& p, hipStream_t st);
+template <typename T, int POLY, int DK, int DV> hipError_t launch_bwd_kv(const KParams& p, hipStream_t st);
+template <typename T, int POLY, int DK, int DV> hipError_t launch_bwd_q(const KParams& p, hipStream_t st);
+
+}  // namespace tnpa

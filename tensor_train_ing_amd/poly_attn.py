@@ -1,0 +1,197 @@
+"""Tiled causal polynomial attention on MI355X: forward and backward through libtnpa.so (HIP, gfx950).
+
+Drop-in for the reference operator ref: tnlm/kernels/poly_attn.py (PolyAttention / poly_attention_triton):
+same argument order, layouts, masking, row normalisation, dtype contract and gradient tuple. Computes, without
+materialising any T x T matrix,
+    y_i = scale_i * sum_{j visible from i} A(S1_ij, S2_ij) v_j,   S_ij = q_i . k_j / sqrt(dk)
+with A one of
+    signed_product   : S1 * S2
+    offset_square    : (S1 + b_h)^2                (q2/k2 unused)
+    lower_degree_mix : c0 + c1 S1 + c2 S2 + c12 S1 S2
+    power            : S1^degree                   (this build's degree-p kind; q2/k2 unused)
+"visible" = causal and same document (doc ids >= 0, contiguous per row); the mask is applied after the
+polynomial; scale_i = n_visible_i^-p is precomputed by the caller (0 for padding queries).
+
+signed_product called with q2 is q1 and k2 is k1 is recognised as degree 2 and computes one QK^T product.
+The only numerical work on the host is argument checking; everything else runs in the HIP kernels.
+"""
+from __future__ import annotations
+
+import ctypes
+
+import torch
+
+from . import _abi
+
+KINDS = {"signed_product": _abi.SIGNED_PRODUCT, "offset_square": _abi.OFFSET_SQUARE,
+         "lower_degree_mix": _abi.LOWER_DEGREE_MIX, "power": _abi.POWER}
+_DTYPES = {torch.bfloat16: _abi.BF16, torch.float32: _abi.F32, torch.float16: _abi.F16}
+_TWO_PAIRS = (_abi.SIGNED_PRODUCT, _abi.LOWER_DEGREE_MIX)
+
+
+def _aligned_rows(x: torch.Tensor) -> bool:
+    """Unit stride on the head dim and 16-byte aligned rows, as the kernels' 128-bit loads require."""
+    es = x.element_size()
+    if x.stride(-1) != 1 or x.data_ptr() % 16 or (x.stride(2) * es) % 16:
+        return False
+    if x.shape[0] > 1 and (x.stride(0) * es) % 16:
+        return False
+    if x.shape[1] > 1 and (x.stride(1) * es) % 16:
+        return False
+    return True
+
+
+def _prep(x: torch.Tensor) -> torch.Tensor:
+    """x itself when the kernels can index it in place, else a contiguous copy (ref: poly_attn.py:262-270)."""
+    return x if _aligned_rows(x) else x.contiguous()
+
+
+def _desc(x: torch.Tensor) -> _abi.Tensor:
+    return _abi.Tensor(x.data_ptr(), x.stride(0), x.stride(1), x.stride(2))
+
+
+def _stream(dev: torch.device) -> ctypes.c_void_p:
+    return ctypes.c_void_p(torch.cuda.current_stream(dev).cuda_stream)
+
+
+def doc_bounds(doc_ids: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
+    """(doc_start, query_end) int32 (B, T): first key visible from each query (q + 1 for padding) and one past the
+    last query that sees each key. Replaces ref: tnlm/kernels/poly_attn.py:205-218 (_block_bounds); int64 ids are
+    read as int64 (no narrowing)."""
+    doc = doc_ids
+    if doc.dtype not in (torch.int32, torch.int64):
+        doc = doc.long()
+    if doc.dim() != 2:
+        raise ValueError(f"doc_ids must be (B, T), got {tuple(doc.shape)}")
+    if doc.stride(1) != 1:
+        doc = doc.contiguous()
+    B, T = doc.shape
+    dstart = torch.empty(B, T, dtype=torch.int32, device=doc.device)
+    qend = torch.empty(B, T, dtype=torch.int32, device=doc.device)
+    lib = _abi.load()
+    with torch.cuda.device(doc.device):
+        _abi.check(lib.tnpa_doc_bounds(ctypes.c_void_p(doc.data_ptr()), int(doc.dtype == torch.int64),
+                                       doc.stride(0), B, T, ctypes.c_void_p(dstart.data_ptr()),
+                                       ctypes.c_void_p(qend.data_ptr()), _stream(doc.device)), "doc_bounds")
+    return dstart, qend
+
+
+def _validate(K, q1, k1, q2, k2, v, doc_ids, row_scale, coef, b, degree):
+    if q1.dim() != 4 or v.dim() != 4:
+        raise ValueError("q*, k*, v must be (B, H, T, d)")
+    B, H, T, DK = q1.shape
+    DV = v.shape[-1]
+    assert DK >= 16 and DK & (DK - 1) == 0 and DV >= 16 and DV & (DV - 1) == 0, "head dims: powers of 2 >= 16"
+    if not q1.is_cuda:
+        raise ValueError("poly_attention_hip needs tensors on a ROCm device")
+    if q1.dtype not in _DTYPES:
+        raise ValueError(f"unsupported dtype {q1.dtype}; expected bfloat16, float16 or float32")
+    used = [("k1", k1), ("v", v)] + ([("q2", q2), ("k2", k2)] if K in _TWO_PAIRS else [])
+    for name, t in used:
+        if t is None:
+            raise ValueError(f"{name} is required for this kind")
+        if t.dtype != q1.dtype or t.device != q1.device:
+            raise ValueError(f"{name}: dtype/device {t.dtype}/{t.device} differs from q1 {q1.dtype}/{q1.device}")
+    for name, t in used[:1] + used[2:]:
+        if tuple(t.shape) != (B, H, T, DK):
+            raise ValueError(f"{name}: shape {tuple(t.shape)}, expected {(B, H, T, DK)}")
+    if tuple(v.shape[:3]) != (B, H, T):
+        raise ValueError(f"v: shape {tuple(v.shape)}, expected {(B, H, T, DV)}")
+    if tuple(doc_ids.shape) != (B, T) or tuple(row_scale.shape) != (B, T):
+        raise ValueError(f"doc_ids and row_scale must be (B, T) = {(B, T)}")
+    if doc_ids.device != q1.device or row_scale.device != q1.device:
+        raise ValueError("doc_ids and row_scale must be on the same device as q1")
+    if row_scale.requires_grad and torch.is_grad_enabled():
+        raise ValueError("row_scale is a fixed position-only factor; a differentiable row_scale is not supported")
+    if K == _abi.LOWER_DEGREE_MIX and (coef is None or tuple(coef.shape) != (H, 4)):
+        raise ValueError("lower_degree_mix needs coef of shape (H, 4)")
+    if K == _abi.OFFSET_SQUARE and (b is None or tuple(b.shape) != (H,)):
+        raise ValueError("offset_square needs b of shape (H,)")
+    if K == _abi.POWER and (degree is None or not 1 <= int(degree) <= 8):
+        raise ValueError("power kind needs degree in 1..8")
+
+
+class PolyAttention(torch.autograd.Function):
+    """ref: tnlm/kernels/poly_attn.py:255-309, with an appended `degree` argument for kind="power"."""
+
+    @staticmethod
+    def forward(ctx, kind, q1, k1, q2, k2, v, doc_ids, row_scale, coef, b, degree=None):
+        K = KINDS[kind]  # unknown kind -> KeyError, as the reference
+        shared = K == _abi.SIGNED_PRODUCT and q2 is q1 and k2 is k1
+        if shared:
+            K, degree = _abi.POWER, 2
+        _validate(K, q1, k1, q2, k2, v, doc_ids, row_scale, coef, b, degree)
+        B, H, T, DK = q1.shape
+        DV = v.shape[-1]
+        q1, k1, v = _prep(q1), _prep(k1), _prep(v)
+        if K in _TWO_PAIRS:
+            q2, k2 = _prep(q2), _prep(k2)
+        else:
+            q2, k2 = q1, k1
+        dstart, qend = doc_bounds(doc_ids)
+        sc = row_scale.detach().float().contiguous()
+        coef_f = coef.detach().float().contiguous() if K == _abi.LOWER_DEGREE_MIX else None
+        b_f = b.detach().float().contiguous() if K == _abi.OFFSET_SQUARE else None
+        o = torch.empty_like(v)
+        if not _aligned_rows(o):
+            o = torch.empty(v.shape, dtype=v.dtype, device=v.device)
+        prob = _problem(K, degree, q1, k1, q2, k2, v, dstart, qend, sc, coef_f, b_f)
+        lib = _abi.load()
+        with torch.cuda.device(q1.device):
+            _abi.check(lib.tnpa_forward(ctypes.byref(prob), ctypes.byref(_desc(o)), _stream(q1.device)),
+                       "poly_attention forward")
+        ctx.save_for_backward(q1, k1, q2, k2, v, dstart, qend, sc, coef_f, b_f)
+        ctx.K, ctx.degree, ctx.shared = K, degree, shared
+        ctx.has_coef, ctx.has_b = coef is not None, b is not None
+        ctx.coef_dtype = coef.dtype if coef is not None else None
+        ctx.b_dtype = b.dtype if b is not None else None
+        return o
+
+    @staticmethod
+    def backward(ctx, do):
+        q1, k1, q2, k2, v, dstart, qend, sc, coef_f, b_f = ctx.saved_tensors
+        K = ctx.K
+        H = q1.shape[1]
+        do = _prep(do.to(v.dtype))
+        dq1, dk1, dv = _alloc_like(q1), _alloc_like(k1), _alloc_like(v)
+        two = K in _TWO_PAIRS
+        dq2, dk2 = (_alloc_like(q2), _alloc_like(k2)) if two else (dq1, dk1)
+        prob = _problem(K, ctx.degree, q1, k1, q2, k2, v, dstart, qend, sc, coef_f, b_f)
+        lib = _abi.load()
+        par = K in (_abi.OFFSET_SQUARE, _abi.LOWER_DEGREE_MIX)
+        ws = dpar = None
+        if par:
+            ws = torch.empty(max(1, lib.tnpa_dpar_workspace_floats(ctypes.byref(prob))), dtype=torch.float32,
+                             device=q1.device)
+            dpar = torch.empty(H, 4, dtype=torch.float32, device=q1.device)
+        g = _abi.Grads(_desc(do), _desc(dq1), _desc(dk1), _desc(dq2), _desc(dk2), _desc(dv),
+                       ws.data_ptr() if par else None, dpar.data_ptr() if par else None)
+        with torch.cuda.device(q1.device):
+            _abi.check(lib.tnpa_backward(ctypes.byref(prob), ctypes.byref(g), _stream(q1.device)),
+                       "poly_attention backward")
+        dcoef = dpar.to(ctx.coef_dtype) if (K == _abi.LOWER_DEGREE_MIX and ctx.has_coef) else None
+        db = dpar[:, 0].to(ctx.b_dtype) if (K == _abi.OFFSET_SQUARE and ctx.has_b) else None
+        if not two:
+            dq2 = dk2 = None
+        return None, dq1, dk1, dq2, dk2, dv, None, None, dcoef, db, None
+
+
+def _alloc_like(x: torch.Tensor) -> torch.Tensor:
+    y = torch.empty_like(x)
+    return y if _aligned_rows(y) else torch.empty(x.shape, dtype=x.dtype, device=x.device)
+
+
+def _problem(K, degree, q1, k1, q2, k2, v, dstart, qend, sc, coef_f, b_f) -> _abi.Problem:
+    B, H, T, DK = q1.shape
+    return _abi.Problem(B, H, T, DK, v.shape[-1], K, int(degree) if degree is not None else 0, _DTYPES[q1.dtype],
+                        _desc(q1), _desc(k1), _desc(q2), _desc(k2), _desc(v),
+                        dstart.data_ptr(), qend.data_ptr(), sc.data_ptr(),
+                        coef_f.data_ptr() if coef_f is not None else None,
+                        b_f.data_ptr() if b_f is not None else None)
+
+
+def poly_attention_hip(kind, q1, k1, q2, k2, v, doc_ids, row_scale, coef=None, b=None, *, degree=None):
+    """q*, k*: (B, H, T, dk); v: (B, H, T, dv); doc_ids: (B, T) contiguous ids, < 0 = padding;
+    row_scale: (B, T) = n_visible^-p for real queries, 0 for padding. kind="power" takes degree=p and ignores
+    q2/k2. Every gradient is reduced in a fixed order (deterministic).  ref: tnlm/kernels/poly_attn.py:312-315"""
+    return PolyAttention.apply(kind, q1, k1, q2, k2, v, doc_ids, row_scale, coef, b, degree)

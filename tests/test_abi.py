@@ -1,0 +1,179 @@
+"""CPU checks of the C ABI (include/tnpa.h) and the host-side operator logic; no GPU compute is launched.
+
+Failure handling the survey asks to force on the CPU: malformed shapes/strides/dtypes/head dims return an error code
+and message before anything is enqueued; a differentiable row_scale is rejected; a missing library fails loudly.
+"""
+from __future__ import annotations
+
+import ctypes
+import re
+import shutil
+import subprocess
+from pathlib import Path
+
+import pytest
+import torch
+
+ROOT = Path(__file__).resolve().parents[1]
+HEADER = ROOT / "include" / "tnpa.h"
+
+
+@pytest.fixture(scope="module")
+def lib():
+    from tensor_train_ing_amd import _abi
+    return _abi.load()
+
+
+def _declared_functions():
+    text = HEADER.read_text()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"^\s*[\w\s\*]+?\b(tnpa_\w+)\s*\(", text, flags=re.M)))
+
+
+def test_library_loads_and_reports_abi_version(lib):
+    from tensor_train_ing_amd import _abi
+    assert lib.tnpa_abi_version() == _abi.ABI_VERSION == 1
+
+
+def test_every_declared_symbol_is_exported(lib):
+    names = _declared_functions()
+    assert len(names) >= 7, names
+    for n in names:
+        assert hasattr(lib, n), n
+    from tensor_train_ing_amd import _abi
+    assert set(_abi._SIGNATURES) == set(names)
+
+
+@pytest.mark.skipif(shutil.which("gcc") is None, reason="needs gcc")
+def test_struct_layout_matches_header(tmp_path):
+    from tensor_train_ing_amd import _abi
+    src = tmp_path / "layout.c"
+    src.write_text(r'''
+#include <stdio.h>
+#include <stddef.h>
+#include "tnpa.h"
+int main(void) {
+  printf("%zu %zu %zu\n", sizeof(tnpa_tensor_t), sizeof(tnpa_problem_t), sizeof(tnpa_grads_t));
+  printf("%zu %zu %zu %zu\n", offsetof(tnpa_problem_t, q1), offsetof(tnpa_problem_t, v),
+         offsetof(tnpa_problem_t, doc_start), offsetof(tnpa_problem_t, offset));
+  printf("%zu %zu\n", offsetof(tnpa_grads_t, dv), offsetof(tnpa_grads_t, dpar));
+  return 0;
+}''')
+    exe = tmp_path / "layout"
+    subprocess.run(["gcc", "-std=c99", "-Wall", "-Werror", "-I", str(ROOT / "include"), str(src), "-o", str(exe)],
+                   check=True)
+    got = [list(map(int, line.split())) for line in subprocess.run([str(exe)], capture_output=True, text=True,
+                                                                     check=True).stdout.splitlines()]
+    P, G = _abi.Problem, _abi.Grads
+    assert got[0] == [ctypes.sizeof(_abi.Tensor), ctypes.sizeof(P), ctypes.sizeof(G)]
+    assert got[1] == [P.q1.offset, P.v.offset, P.doc_start.offset, P.offset.offset]
+    assert got[2] == [G.dv.offset, G.dpar.offset]
+
+
+def _problem(**kw):
+    from tensor_train_ing_amd import _abi
+    t = _abi.Tensor(4096, 2 * 128 * 64, 128 * 64, 64)  # an aligned (never dereferenced) fake address
+    p = _abi.Problem(2, 2, 128, 64, 64, _abi.POWER, 2, _abi.BF16, t, t, t, t, t, 4096, 4096, 4096, None, None)
+    for k, v in kw.items():
+        setattr(p, k, v)
+    return p
+
+
+@pytest.mark.parametrize("field,value,code,msg", [
+    ("batch", 0, 1, "positive"),
+    ("head_dim_k", 24, 1, "powers of 2"),
+    ("head_dim_v", 8, 1, "powers of 2"),
+    ("head_dim_k", 256, 2, "above 128"),
+    ("kind", 7, 1, "unknown kind"),
+    ("degree", 0, 1, "degree"),
+    ("dtype", 9, 1, "dtype"),
+    ("doc_start", None, 1, "tnpa_doc_bounds"),
+    ("row_scale", None, 1, "row_scale"),
+])
+def test_forward_rejects_bad_arguments_before_launch(lib, field, value, code, msg):
+    from tensor_train_ing_amd import _abi
+    p = _problem(**{field: value})
+    out = _abi.Tensor(4096, 2 * 128 * 64, 128 * 64, 64)
+    assert lib.tnpa_forward(ctypes.byref(p), ctypes.byref(out), None) == code
+    assert msg in lib.tnpa_last_error().decode()
+
+
+def test_misaligned_views_and_missing_parameters_are_rejected(lib):
+    from tensor_train_ing_amd import _abi
+    out = _abi.Tensor(4096, 2 * 128 * 64, 128 * 64, 64)
+    p = _problem(q1=_abi.Tensor(4098, 2 * 128 * 64, 128 * 64, 64))
+    assert lib.tnpa_forward(ctypes.byref(p), ctypes.byref(out), None) == _abi.ERR_INVALID
+    assert "aligned" in lib.tnpa_last_error().decode()
+    p = _problem(v=_abi.Tensor(4096, 2 * 128 * 64, 128 * 64, 60))
+    assert lib.tnpa_forward(ctypes.byref(p), ctypes.byref(out), None) == _abi.ERR_INVALID
+    p = _problem(kind=_abi.LOWER_DEGREE_MIX)
+    assert lib.tnpa_forward(ctypes.byref(p), ctypes.byref(out), None) == _abi.ERR_INVALID
+    assert "coef" in lib.tnpa_last_error().decode()
+    p = _problem(kind=_abi.OFFSET_SQUARE)
+    assert lib.tnpa_forward(ctypes.byref(p), ctypes.byref(out), None) == _abi.ERR_INVALID
+    assert "offset" in lib.tnpa_last_error().decode()
+    assert lib.tnpa_forward(None, ctypes.byref(out), None) == _abi.ERR_INVALID
+    # backward: the two head-scalar kinds need the dpar buffers
+    p = _problem(kind=_abi.OFFSET_SQUARE, offset=4096)
+    t = _abi.Tensor(4096, 2 * 128 * 64, 128 * 64, 64)
+    g = _abi.Grads(t, t, t, t, t, t, None, None)
+    assert lib.tnpa_backward(ctypes.byref(p), ctypes.byref(g), None) == _abi.ERR_INVALID
+    assert "dpar" in lib.tnpa_last_error().decode()
+    assert lib.tnpa_backward_phase(ctypes.byref(_problem()), ctypes.byref(g), 0, None) == _abi.ERR_INVALID
+    assert lib.tnpa_backward_phase(ctypes.byref(_problem()), ctypes.byref(g), 4, None) == _abi.ERR_INVALID
+    assert lib.tnpa_doc_bounds(None, 1, 128, 2, 128, None, None, None) == _abi.ERR_INVALID
+    assert lib.tnpa_doc_bounds(ctypes.c_void_p(4096), 1, 64, 2, 128, ctypes.c_void_p(4096), ctypes.c_void_p(4096),
+                               None) == _abi.ERR_INVALID
+
+
+def test_dpar_workspace_size(lib):
+    from tensor_train_ing_amd import _abi
+    assert lib.tnpa_dpar_workspace_floats(ctypes.byref(_problem())) == 0
+    p = _problem(kind=_abi.LOWER_DEGREE_MIX, seq_len=300)
+    assert lib.tnpa_dpar_workspace_floats(ctypes.byref(p)) == 2 * 2 * 3 * 4  # ceil(300 / 128) key blocks
+
+
+def test_python_operator_errors_mirror_the_reference():
+    from tensor_train_ing_amd import poly_attention_hip
+    x = torch.zeros(1, 1, 8, 16)
+    doc, rs = torch.zeros(1, 8, dtype=torch.long), torch.ones(1, 8)
+    with pytest.raises(KeyError):
+        poly_attention_hip("softmax", x, x, x, x, x, doc, rs)
+    with pytest.raises(AssertionError, match="powers of 2"):
+        y = torch.zeros(1, 1, 8, 24)
+        poly_attention_hip("signed_product", y, y, y, y, y, doc, rs)
+    with pytest.raises(ValueError, match="ROCm device"):
+        poly_attention_hip("signed_product", x, x, x, x, x, doc, rs)
+
+
+def test_differentiable_row_scale_is_rejected():
+    from tensor_train_ing_amd.poly_attn import _abi as abi_mod, _validate
+    x = torch.zeros(1, 1, 8, 16)
+    rs = torch.ones(1, 8, requires_grad=True)
+    with pytest.raises(ValueError):
+        _validate(abi_mod.POWER, x, x, None, None, x, torch.zeros(1, 8, dtype=torch.long), rs, None, None, 2)
+
+
+def test_missing_library_fails_loudly(tmp_path):
+    from tensor_train_ing_amd import _abi
+    with pytest.raises(RuntimeError, match="missing"):
+        _abi.load(tmp_path / "libtnpa.so")
+
+
+def test_backend_resolution_mirrors_reference():
+    from tensor_train_ing_amd import ATTENTION_BACKENDS, resolve_attention_backend
+    assert ATTENTION_BACKENDS == ("reference", "triton", "hip", "auto")
+    assert resolve_attention_backend("auto", "cpu") == "reference"
+    assert resolve_attention_backend("auto", "cpu", "softmax") == "softmax"
+    expect = "hip" if torch.version.hip is not None else "triton"
+    assert resolve_attention_backend("auto", "cuda:0") == expect
+    assert resolve_attention_backend("hip", "cuda:0", "softmax") == "flex"
+    assert resolve_attention_backend("reference", "cuda:0") == "reference"
+    with pytest.raises(AssertionError):
+        resolve_attention_backend("cuda", "cpu")
+
+
+def test_product_never_imports_the_oracle():
+    for f in (ROOT / "tensor_train_ing_amd").rglob("*.py"):
+        src = f.read_text()
+        assert not re.search(r"^\s*(from|import)\s+oracle\b", src, flags=re.M), f
