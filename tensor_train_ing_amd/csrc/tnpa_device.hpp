@@ -104,47 +104,52 @@ template <typename T> __device__ constexpr inline int kappa(int i) {
 }
 
 // ------------------------------------------------------------------------------------------------ LDS tiles
-// Row-major ROWS x WID tile of T, WID a multiple of 32 (head dims below 32 are zero padded). Stored in 16-byte
-// chunks with chunk index XOR-swizzled by row.
+// Row-major ROWS x WID tile of T (WID a multiple of 32; head dims below 32 are zero padded). Rows are padded by
+// 16 bytes and, for 16-bit types, permuted inside each 16-row group by prow(): logical row l is stored at
+// 4*(l%4) + 2*((l/8)%2) + (l/4)%2. With that pitch and permutation both access patterns are bank-conflict free:
+// the row reads (16 lanes reading 16 different rows of one 16-byte column chunk) and the transposed reads (each
+// half-wave reading 4 rows k0+4s+0..3 of 64 bytes, which land 16 banks apart). Every offset is a per-lane base
+// plus a compile-time immediate, so the kernels keep one address register per access pattern.
 template <typename T, int ROWS, int WID> struct Tile {
-  static constexpr int CE = 16 / (int)sizeof(T);  // elements per 16-byte chunk
-  static constexpr int NCH = WID / CE;            // chunks per row
-  static constexpr int BYTES = ROWS * WID * (int)sizeof(T);
-  static_assert(NCH >= 4 && (NCH & (NCH - 1)) == 0, "tile width");
-  __device__ static inline int swz(int r) {
-    if constexpr (NCH >= 16) return ((r & 3) << 2) | ((r >> 2) & 3);
-    else if constexpr (NCH == 8) return (((r >> 1) & 1) << 2) | ((r >> 2) & 3);
-    else return (r >> 2) & 3;
+  static constexpr int PITCH = WID * (int)sizeof(T) + 16;  // bytes per row
+  static constexpr int BYTES = ROWS * PITCH;
+  static_assert(WID % 32 == 0, "tile width");
+  __device__ static constexpr int prow(int r) {
+    if constexpr (sizeof(T) == 2) {
+      const int l = r & 15;
+      return (r & ~15) | (4 * (l & 3) + 2 * ((l >> 3) & 1) + ((l >> 2) & 1));
+    } else {
+      return r;
+    }
   }
   // byte offset of element (r, col)
-  __device__ static inline uint32_t off(int r, int col) {
-    const int ch = col / CE, e = col % CE;
-    return (uint32_t)(((r * NCH + (ch ^ swz(r))) * 16) + e * (int)sizeof(T));
-  }
+  __device__ static inline uint32_t off(int r, int col) { return (uint32_t)(prow(r) * PITCH + col * (int)sizeof(T)); }
 };
 
-// A/B operand whose contraction runs along the row (head dim): elements [c*KC + h*EPL, +EPL) of tile row `row`.
+// A/B operand whose contraction runs along the row (head dim): elements [c*KC + h*EPL, +EPL) of tile row
+// rbase + lrow, where rbase is a multiple of 16 shared by the wave and lrow in [0, 32) is per lane.
 template <typename T, typename TL>
-__device__ inline typename Mfma<T>::Op read_row(const char TNPA_LDS* tile, int row, int c, int h) {
+__device__ inline typename Mfma<T>::Op read_row(const char TNPA_LDS* tile, int rbase, int lrow, int c, int h) {
   typedef typename Mfma<T>::Op Op;
   const int col = c * Mfma<T>::KC + h * Mfma<T>::EPL;
-  return *(const Op TNPA_LDS*)(tile + TL::off(row, col));
+  return *(const Op TNPA_LDS*)(tile + rbase * TL::PITCH + TL::prow(lrow) * TL::PITCH + col * (int)sizeof(T));
 }
 
-// A/B operand whose contraction runs down the rows: lane (n = l%32, h) gets tile[k0 + h*EPL + j][col0 + n].
+// A/B operand whose contraction runs down the rows: lane (n = l%32, h) gets tile[k0 + h*EPL + j][col0 + n]
+// (k0 a multiple of 16 for 16-bit types).
 template <typename T, typename TL>
 __device__ inline typename Mfma<T>::Op read_col(const char TNPA_LDS* tile, int k0, int col0, int lane) {
   typedef typename Mfma<T>::Op Op;
   if constexpr (sizeof(T) == 2) {
+    // logical rows k0 + 8*hh + 4*s + (i>>2) sit at physical rows k0 + 4*(i>>2) + 2*hh + s
     const int i = lane & 15, g = lane >> 4, hh = lane >> 5;
-    const int col = col0 + 16 * (g & 1) + 4 * (i & 3);
-    const int row = k0 + 8 * hh + (i >> 2);
-    s16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((s16x4 TNPA_LDS*)(tile + TL::off(row, col)));
-    s16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((s16x4 TNPA_LDS*)(tile + TL::off(row + 4, col)));
+    const char TNPA_LDS* p = tile + (k0 + 4 * (i >> 2) + 2 * hh) * TL::PITCH + (col0 + 16 * (g & 1) + 4 * (i & 3)) * 2;
+    s16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((s16x4 TNPA_LDS*)p);
+    s16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((s16x4 TNPA_LDS*)(p + TL::PITCH));
     s16x8 both = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
     return __builtin_bit_cast(Op, both);
   } else {
-    return *(const float TNPA_LDS*)(tile + TL::off(k0 + (lane >> 5), col0 + (lane & 31)));
+    return *(const float TNPA_LDS*)(tile + (k0 + (lane >> 5)) * TL::PITCH + (col0 + (lane & 31)) * 4);
   }
 }
 

@@ -22,6 +22,7 @@
 #pragma once
 
 #include <climits>
+#include <type_traits>
 
 #include "tnpa_device.hpp"
 #include "tnpa_params.hpp"
@@ -95,6 +96,10 @@ __device__ inline void poly_grad(float r1, float r2, float hg, int kind, int deg
   }
 }
 
+// A condition every lane of the wave evaluates identically, moved to a scalar register so the compiler branches
+// on it without exec masking.
+__device__ inline bool uniform_bool(bool c) { return __builtin_amdgcn_readfirstlane((int)c) != 0; }
+
 template <typename T> __device__ inline const T* head_ptr(const TDesc& d, int b, int hd) {
   return (const T*)d.p + (int64_t)b * d.sb + (int64_t)hd * d.sh;
 }
@@ -103,19 +108,22 @@ template <typename T> __device__ inline T* head_ptr_w(const TDesc& d, int b, int
 }
 
 // ------------------------------------------------------------------------------------------------ tile configs
+// NW waves per workgroup, QW / KW 32-row subtiles per wave, BN / BM rows per LDS tile, WPE = waves per SIMD the
+// register allocation must allow (2 lets a second wave hide the first one's LDS latency).
 template <typename T, int POLY, int DK, int DV> struct Cfg {
   static constexpr bool F32 = sizeof(T) == 4;
   static constexpr int NPAIR = POLY == POLY_GEN2 ? 2 : 1;
-  static constexpr int FW_NW = 4, FW_QW = F32 ? 1 : 2, FW_BN = F32 ? 32 : 64;
-  static constexpr int BQ_NW = 4, BQ_QW = (F32 || NPAIR == 2) ? 1 : 2, BQ_BN = F32 ? 32 : 64;
-  static constexpr int KV_NW = 4, KV_KW = 1, KV_BM = F32 ? 32 : 64;
+  static constexpr int FW_NW = 4, FW_QW = 1, FW_BN = F32 ? 32 : 64, FW_WPE = (F32 || NPAIR == 2) ? 1 : 2;
+  static constexpr int BQ_NW = 4, BQ_QW = 1, BQ_BN = F32 ? 32 : 64, BQ_WPE = (F32 || NPAIR == 2) ? 1 : 2;
+  static constexpr int KV_NW = 4, KV_KW = 1, KV_BM = F32 ? 32 : 64, KV_WPE = 1;
   static constexpr int KV_KEYS = KV_NW * KV_KW * 32;
 };
 
 // ------------------------------------------------------------------------------------------------ forward
 // ref: tnlm/kernels/poly_attn.py:37-74 (_fwd)
-template <typename T, int POLY, int DK, int DV, int NW, int QW, int BN>
-__global__ void __launch_bounds__(NW * 64) k_fwd(const KParams p) {
+template <typename T, int POLY, int DK, int DV, int NW, int QW, int BN, int WPE>
+__global__ void __attribute__((amdgpu_flat_work_group_size(NW * 64, NW * 64), amdgpu_waves_per_eu(WPE)))
+k_fwd(const KParams p) {
   typedef Mfma<T> M;
   typedef typename M::Op Op;
   constexpr int KC = M::KC, EPL = M::EPL, NT = NW * 64;
@@ -188,7 +196,59 @@ __global__ void __launch_bounds__(NW * 64) k_fwd(const KParams p) {
   __syncthreads();
 
   int cur = 0;
-  for (int n0 = lo; n0 < hi; n0 += BN) {
+  auto sub = [&](const char TNPA_LDS* base, const int n0, const int kb, const uint32_t am, const uint32_t fm, auto all_c, auto full_c) {
+    constexpr bool ALL = decltype(all_c)::value, FULL = decltype(full_c)::value;
+    const int key0 = n0 + 32 * kb;
+    f32x16 sacc[NPAIR][QW];
+#pragma unroll
+    for (int pr = 0; pr < NPAIR; ++pr)
+#pragma unroll
+      for (int s = 0; s < QW; ++s) sacc[pr][s] = zero16();
+#pragma unroll
+    for (int c = 0; c < NCK; ++c)
+#pragma unroll
+      for (int pr = 0; pr < NPAIR; ++pr) {
+        const Op a = read_row<T, KTile>(base + pr * KTile::BYTES, 32 * kb, kappa<T>(l32), c, h);
+#pragma unroll
+        for (int s = 0; s < QW; ++s)
+          if (ALL || ((am >> s) & 1u)) sacc[pr][s] = M::mma(a, qf[pr][s][c], sacc[pr][s]);
+      }
+    Op pop[QW][NC2];
+#pragma unroll
+    for (int s = 0; s < QW; ++s) {
+      if (!(ALL || ((am >> s) & 1u))) continue;
+      float pv[16];
+      if (FULL || ((fm >> s) & 1u)) {
+#pragma unroll
+        for (int r = 0; r < 16; ++r)
+          pv[r] = poly_value<POLY>(sacc[0][s][r], sacc[NPAIR - 1][s][r], p.kind, p.deg, p.sm, cf);
+      } else {
+        const int q = qa[s] + l32;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int key = key0 + key_off<T>(r, h);
+          const float val = poly_value<POLY>(sacc[0][s][r], sacc[NPAIR - 1][s][r], p.kind, p.deg, p.sm, cf);
+          pv[r] = (key > q || key < dsq[s]) ? 0.f : val;
+        }
+      }
+#pragma unroll
+      for (int c2 = 0; c2 < NC2; ++c2) pop[s][c2] = M::cvt(pv + c2 * EPL);
+    }
+#pragma unroll
+    for (int d = 0; d < NDV; ++d)
+#pragma unroll
+      for (int c2 = 0; c2 < NC2; ++c2) {
+        const Op a = read_col<T, VTile>(base + NPAIR * KTile::BYTES, 32 * kb + c2 * KC, 32 * d, lane);
+#pragma unroll
+        for (int s = 0; s < QW; ++s)
+          if (ALL || ((am >> s) & 1u)) oacc[s][d] = M::mma(a, pop[s][c2], oacc[s][d]);
+      }
+  };
+
+  // One tile step: prefetch the next K/V tile into registers, compute on the current LDS buffer, publish the
+  // prefetched tile into the other buffer, one barrier.
+  auto step = [&](const int n0, auto fast_c) {
+    constexpr bool FAST = decltype(fast_c)::value;
     const bool more = n0 + BN < hi;
     if (more) {
 #pragma unroll
@@ -196,60 +256,24 @@ __global__ void __launch_bounds__(NW * 64) k_fwd(const KParams p) {
       sv.load(vp, p.v.st, n0 + BN, T_ - n0 - BN);
     }
     const char TNPA_LDS* base = smem + cur * BUF;
+    if constexpr (FAST) {
 #pragma unroll
-    for (int kb = 0; kb < NKB; ++kb) {
-      const int key0 = n0 + 32 * kb;
-      bool act[QW];
-      bool any = false;
+      for (int kb = 0; kb < NKB; ++kb) sub(base, n0, kb, 0u, 0u, std::true_type{}, std::true_type{});
+    } else {
 #pragma unroll
-      for (int s = 0; s < QW; ++s) {
-        act[s] = qa[s] < T_ && key0 <= ql[s] && key0 + 31 >= dsa[s];
-        any |= act[s];
+      for (int kb = 0; kb < NKB; ++kb) {
+        const int key0 = n0 + 32 * kb;
+        uint32_t am = 0, fm = 0;
+#pragma unroll
+        for (int s = 0; s < QW; ++s) {
+          if (qa[s] < T_ && key0 <= ql[s] && key0 + 31 >= dsa[s]) am |= 1u << s;
+          if (key0 + 31 <= qa[s] && dsl[s] <= key0) fm |= 1u << s;
+        }
+        am = __builtin_amdgcn_readfirstlane(am);
+        fm = __builtin_amdgcn_readfirstlane(fm);
+        if (am == 0) continue;
+        sub(base, n0, kb, am, fm, std::false_type{}, std::false_type{});
       }
-      if (!any) continue;
-      f32x16 sacc[NPAIR][QW];
-#pragma unroll
-      for (int pr = 0; pr < NPAIR; ++pr)
-#pragma unroll
-        for (int s = 0; s < QW; ++s) sacc[pr][s] = zero16();
-      const int krow = 32 * kb + kappa<T>(l32);
-#pragma unroll
-      for (int c = 0; c < NCK; ++c)
-#pragma unroll
-        for (int pr = 0; pr < NPAIR; ++pr) {
-          const Op a = read_row<T, KTile>(base + pr * KTile::BYTES, krow, c, h);
-#pragma unroll
-          for (int s = 0; s < QW; ++s)
-            if (act[s]) sacc[pr][s] = M::mma(a, qf[pr][s][c], sacc[pr][s]);
-        }
-      Op pop[QW][NC2];
-#pragma unroll
-      for (int s = 0; s < QW; ++s) {
-        if (!act[s]) continue;
-        const bool full = key0 + 31 <= qa[s] && dsl[s] <= key0;
-        const int q = qa[s] + l32;
-        float pv[16];
-#pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          float val = poly_value<POLY>(sacc[0][s][r], sacc[NPAIR - 1][s][r], p.kind, p.deg, p.sm, cf);
-          if (!full) {
-            const int key = key0 + key_off<T>(r, h);
-            if (key > q || key < dsq[s]) val = 0.f;
-          }
-          pv[r] = val;
-        }
-#pragma unroll
-        for (int c2 = 0; c2 < NC2; ++c2) pop[s][c2] = M::cvt(pv + c2 * EPL);
-      }
-#pragma unroll
-      for (int d = 0; d < NDV; ++d)
-#pragma unroll
-        for (int c2 = 0; c2 < NC2; ++c2) {
-          const Op a = read_col<T, VTile>(base + NPAIR * KTile::BYTES, 32 * kb + c2 * KC, 32 * d, lane);
-#pragma unroll
-          for (int s = 0; s < QW; ++s)
-            if (act[s]) oacc[s][d] = M::mma(a, pop[s][c2], oacc[s][d]);
-        }
     }
     if (more) {
       char TNPA_LDS* nxt = smem + (cur ^ 1) * BUF;
@@ -259,7 +283,23 @@ __global__ void __launch_bounds__(NW * 64) k_fwd(const KParams p) {
     }
     __syncthreads();
     cur ^= 1;
+  };
+  // Tiles lo, lo+BN, ... < hi, split per wave into three contiguous runs: before the document start of the
+  // wave's last query (generic), fully visible from every query of the wave (fast: no mask, no per-subtile test),
+  // and the diagonal (generic). Every wave steps through all tiles, so the barrier count matches across waves.
+  const int ntile = (hi - lo + BN - 1) / BN;
+  int j0 = 0, j1 = 0;
+  if (qa[0] < T_) {
+    const int dl = dst[min(qw0 + 32 * QW - 1, T_ - 1)];
+    j0 = min(ntile, max(0, (dl - lo + BN - 1) / BN));
+    j1 = max(j0, min(ntile, (qa[0] + 1 - lo) / BN));
   }
+  j0 = __builtin_amdgcn_readfirstlane(j0);
+  j1 = __builtin_amdgcn_readfirstlane(j1);
+  int j = 0;
+  for (; j < j0; ++j) step(lo + j * BN, std::false_type{});
+  for (; j < j1; ++j) step(lo + j * BN, std::true_type{});
+  for (; j < ntile; ++j) step(lo + j * BN, std::false_type{});
 
   T* op = head_ptr_w<T>(p.o, b, hd);
 #pragma unroll
@@ -282,8 +322,9 @@ __global__ void __launch_bounds__(NW * 64) k_fwd(const KParams p) {
 
 // ------------------------------------------------------------------------------------------------ dQ
 // ref: tnlm/kernels/poly_attn.py:151-202 (_bwd_q)
-template <typename T, int POLY, int DK, int DV, int NW, int QW, int BN>
-__global__ void __launch_bounds__(NW * 64) k_bwd_q(const KParams p) {
+template <typename T, int POLY, int DK, int DV, int NW, int QW, int BN, int WPE>
+__global__ void __attribute__((amdgpu_flat_work_group_size(NW * 64, NW * 64), amdgpu_waves_per_eu(WPE)))
+k_bwd_q(const KParams p) {
   typedef Mfma<T> M;
   typedef typename M::Op Op;
   constexpr int KC = M::KC, EPL = M::EPL, NT = NW * 64;
@@ -362,7 +403,75 @@ __global__ void __launch_bounds__(NW * 64) k_bwd_q(const KParams p) {
   __syncthreads();
 
   int cur = 0;
-  for (int n0 = lo; n0 < hi; n0 += BN) {
+  auto sub = [&](const char TNPA_LDS* base, const int n0, const int kb, const uint32_t am, const uint32_t fm, auto all_c, auto full_c) {
+    constexpr bool ALL = decltype(all_c)::value, FULL = decltype(full_c)::value;
+    const int key0 = n0 + 32 * kb;
+    f32x16 sacc[NPAIR][QW], pacc[QW];
+#pragma unroll
+    for (int s = 0; s < QW; ++s) {
+      pacc[s] = zero16();
+#pragma unroll
+      for (int pr = 0; pr < NPAIR; ++pr) sacc[pr][s] = zero16();
+    }
+#pragma unroll
+    for (int c = 0; c < NCK; ++c)
+#pragma unroll
+      for (int pr = 0; pr < NPAIR; ++pr) {
+        const Op a = read_row<T, KTile>(base + pr * KTile::BYTES, 32 * kb, kappa<T>(l32), c, h);
+#pragma unroll
+        for (int s = 0; s < QW; ++s)
+          if (ALL || ((am >> s) & 1u)) sacc[pr][s] = M::mma(a, qf[pr][s][c], sacc[pr][s]);
+      }
+#pragma unroll
+    for (int c = 0; c < NCV; ++c) {
+      const Op a = read_row<T, VTile>(base + NPAIR * KTile::BYTES, 32 * kb, kappa<T>(l32), c, h);
+#pragma unroll
+      for (int s = 0; s < QW; ++s)
+        if (ALL || ((am >> s) & 1u)) pacc[s] = M::mma(a, dof[s][c], pacc[s]);
+    }
+    Op dso[NPAIR][QW][NC2];
+#pragma unroll
+    for (int s = 0; s < QW; ++s) {
+      if (!(ALL || ((am >> s) & 1u))) continue;
+      float d1[16], d2[16];
+      if (FULL || ((fm >> s) & 1u)) {
+#pragma unroll
+        for (int r = 0; r < 16; ++r)
+          poly_grad<POLY, false>(sacc[0][s][r], sacc[NPAIR - 1][s][r], pacc[s][r], p.kind, p.deg, p.sm, cf, d1[r],
+                                 d2[r], nullptr);
+      } else {
+        const int q = qa[s] + l32;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int key = key0 + key_off<T>(r, h);
+          const float hg = (key > q || key < dsq[s]) ? 0.f : pacc[s][r];
+          poly_grad<POLY, false>(sacc[0][s][r], sacc[NPAIR - 1][s][r], hg, p.kind, p.deg, p.sm, cf, d1[r], d2[r],
+                                 nullptr);
+        }
+      }
+#pragma unroll
+      for (int c2 = 0; c2 < NC2; ++c2) {
+        dso[0][s][c2] = M::cvt(d1 + c2 * EPL);
+        if constexpr (NPAIR == 2) dso[NPAIR - 1][s][c2] = M::cvt(d2 + c2 * EPL);
+      }
+    }
+#pragma unroll
+    for (int pr = 0; pr < NPAIR; ++pr)
+#pragma unroll
+      for (int d = 0; d < NDK; ++d)
+#pragma unroll
+        for (int c2 = 0; c2 < NC2; ++c2) {
+          const Op a = read_col<T, KTile>(base + pr * KTile::BYTES, 32 * kb + c2 * KC, 32 * d, lane);
+#pragma unroll
+          for (int s = 0; s < QW; ++s)
+            if (ALL || ((am >> s) & 1u)) dq[pr][s][d] = M::mma(a, dso[pr][s][c2], dq[pr][s][d]);
+        }
+  };
+
+  // One tile step: prefetch the next K/V tile into registers, compute on the current LDS buffer, publish the
+  // prefetched tile into the other buffer, one barrier.
+  auto step = [&](const int n0, auto fast_c) {
+    constexpr bool FAST = decltype(fast_c)::value;
     const bool more = n0 + BN < hi;
     if (more) {
 #pragma unroll
@@ -370,75 +479,24 @@ __global__ void __launch_bounds__(NW * 64) k_bwd_q(const KParams p) {
       sv.load(vp, p.v.st, n0 + BN, T_ - n0 - BN);
     }
     const char TNPA_LDS* base = smem + cur * BUF;
+    if constexpr (FAST) {
 #pragma unroll
-    for (int kb = 0; kb < NKB; ++kb) {
-      const int key0 = n0 + 32 * kb;
-      bool act[QW];
-      bool any = false;
+      for (int kb = 0; kb < NKB; ++kb) sub(base, n0, kb, 0u, 0u, std::true_type{}, std::true_type{});
+    } else {
 #pragma unroll
-      for (int s = 0; s < QW; ++s) {
-        act[s] = qa[s] < T_ && key0 <= ql[s] && key0 + 31 >= dsa[s];
-        any |= act[s];
-      }
-      if (!any) continue;
-      f32x16 sacc[NPAIR][QW], pacc[QW];
+      for (int kb = 0; kb < NKB; ++kb) {
+        const int key0 = n0 + 32 * kb;
+        uint32_t am = 0, fm = 0;
 #pragma unroll
-      for (int s = 0; s < QW; ++s) {
-        pacc[s] = zero16();
-#pragma unroll
-        for (int pr = 0; pr < NPAIR; ++pr) sacc[pr][s] = zero16();
-      }
-      const int krow = 32 * kb + kappa<T>(l32);
-#pragma unroll
-      for (int c = 0; c < NCK; ++c)
-#pragma unroll
-        for (int pr = 0; pr < NPAIR; ++pr) {
-          const Op a = read_row<T, KTile>(base + pr * KTile::BYTES, krow, c, h);
-#pragma unroll
-          for (int s = 0; s < QW; ++s)
-            if (act[s]) sacc[pr][s] = M::mma(a, qf[pr][s][c], sacc[pr][s]);
+        for (int s = 0; s < QW; ++s) {
+          if (qa[s] < T_ && key0 <= ql[s] && key0 + 31 >= dsa[s]) am |= 1u << s;
+          if (key0 + 31 <= qa[s] && dsl[s] <= key0) fm |= 1u << s;
         }
-#pragma unroll
-      for (int c = 0; c < NCV; ++c) {
-        const Op a = read_row<T, VTile>(base + NPAIR * KTile::BYTES, krow, c, h);
-#pragma unroll
-        for (int s = 0; s < QW; ++s)
-          if (act[s]) pacc[s] = M::mma(a, dof[s][c], pacc[s]);
+        am = __builtin_amdgcn_readfirstlane(am);
+        fm = __builtin_amdgcn_readfirstlane(fm);
+        if (am == 0) continue;
+        sub(base, n0, kb, am, fm, std::false_type{}, std::false_type{});
       }
-      Op dso[NPAIR][QW][NC2];
-#pragma unroll
-      for (int s = 0; s < QW; ++s) {
-        if (!act[s]) continue;
-        const bool full = key0 + 31 <= qa[s] && dsl[s] <= key0;
-        const int q = qa[s] + l32;
-        float d1[16], d2[16];
-#pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          float hg = pacc[s][r];
-          if (!full) {
-            const int key = key0 + key_off<T>(r, h);
-            if (key > q || key < dsq[s]) hg = 0.f;
-          }
-          poly_grad<POLY, false>(sacc[0][s][r], sacc[NPAIR - 1][s][r], hg, p.kind, p.deg, p.sm, cf, d1[r], d2[r],
-                                 nullptr);
-        }
-#pragma unroll
-        for (int c2 = 0; c2 < NC2; ++c2) {
-          dso[0][s][c2] = M::cvt(d1 + c2 * EPL);
-          if constexpr (NPAIR == 2) dso[NPAIR - 1][s][c2] = M::cvt(d2 + c2 * EPL);
-        }
-      }
-#pragma unroll
-      for (int pr = 0; pr < NPAIR; ++pr)
-#pragma unroll
-        for (int d = 0; d < NDK; ++d)
-#pragma unroll
-          for (int c2 = 0; c2 < NC2; ++c2) {
-            const Op a = read_col<T, KTile>(base + pr * KTile::BYTES, 32 * kb + c2 * KC, 32 * d, lane);
-#pragma unroll
-            for (int s = 0; s < QW; ++s)
-              if (act[s]) dq[pr][s][d] = M::mma(a, dso[pr][s][c2], dq[pr][s][d]);
-          }
     }
     if (more) {
       char TNPA_LDS* nxt = smem + (cur ^ 1) * BUF;
@@ -448,7 +506,23 @@ __global__ void __launch_bounds__(NW * 64) k_bwd_q(const KParams p) {
     }
     __syncthreads();
     cur ^= 1;
+  };
+  // Tiles lo, lo+BN, ... < hi, split per wave into three contiguous runs: before the document start of the
+  // wave's last query (generic), fully visible from every query of the wave (fast: no mask, no per-subtile test),
+  // and the diagonal (generic). Every wave steps through all tiles, so the barrier count matches across waves.
+  const int ntile = (hi - lo + BN - 1) / BN;
+  int j0 = 0, j1 = 0;
+  if (qa[0] < T_) {
+    const int dl = dst[min(qw0 + 32 * QW - 1, T_ - 1)];
+    j0 = min(ntile, max(0, (dl - lo + BN - 1) / BN));
+    j1 = max(j0, min(ntile, (qa[0] + 1 - lo) / BN));
   }
+  j0 = __builtin_amdgcn_readfirstlane(j0);
+  j1 = __builtin_amdgcn_readfirstlane(j1);
+  int j = 0;
+  for (; j < j0; ++j) step(lo + j * BN, std::false_type{});
+  for (; j < j1; ++j) step(lo + j * BN, std::true_type{});
+  for (; j < ntile; ++j) step(lo + j * BN, std::false_type{});
 
   const TDesc* outs[2] = {&p.dq1, &p.dq2};
 #pragma unroll
@@ -475,8 +549,9 @@ __global__ void __launch_bounds__(NW * 64) k_bwd_q(const KParams p) {
 
 // ------------------------------------------------------------------------------------------------ dK / dV
 // ref: tnlm/kernels/poly_attn.py:77-148 (_bwd_kv)
-template <typename T, int POLY, int DK, int DV, int NW, int KW, int BMQ>
-__global__ void __launch_bounds__(NW * 64) k_bwd_kv(const KParams p) {
+template <typename T, int POLY, int DK, int DV, int NW, int KW, int BMQ, int WPE>
+__global__ void __attribute__((amdgpu_flat_work_group_size(NW * 64, NW * 64), amdgpu_waves_per_eu(WPE)))
+k_bwd_kv(const KParams p) {
   typedef Mfma<T> M;
   typedef typename M::Op Op;
   constexpr int KC = M::KC, EPL = M::EPL, NT = NW * 64;
@@ -559,7 +634,88 @@ __global__ void __launch_bounds__(NW * 64) k_bwd_kv(const KParams p) {
   __syncthreads();
 
   int cur = 0;
-  for (int m = qlo; m < qhi; m += BMQ) {
+  // One 32-query sub-block for this wave. am / fm: wave-uniform bitmasks of the key subtiles seen by any query of
+  // the sub-block / seen by all of them.
+  auto sub = [&](const char TNPA_LDS* base, const int TNPA_LDS* dsl, const int m, const int qb, const uint32_t am, const uint32_t fm, auto all_c, auto full_c) {
+    constexpr bool ALL = decltype(all_c)::value, FULL = decltype(full_c)::value;
+    f32x16 sacc[NPAIR][KW], pacc[KW];
+#pragma unroll
+    for (int s = 0; s < KW; ++s) {
+      pacc[s] = zero16();
+#pragma unroll
+      for (int pr = 0; pr < NPAIR; ++pr) sacc[pr][s] = zero16();
+    }
+#pragma unroll
+    for (int c = 0; c < NCK; ++c)
+#pragma unroll
+      for (int pr = 0; pr < NPAIR; ++pr) {
+        const Op a = read_row<T, QTile>(base + pr * QTile::BYTES, 32 * qb, kappa<T>(l32), c, h);
+#pragma unroll
+        for (int s = 0; s < KW; ++s)
+          if (ALL || ((am >> s) & 1u)) sacc[pr][s] = M::mma(a, kf[pr][s][c], sacc[pr][s]);
+      }
+#pragma unroll
+    for (int c = 0; c < NCV; ++c) {
+      const Op a = read_row<T, OTile>(base + NPAIR * QTile::BYTES, 32 * qb, kappa<T>(l32), c, h);
+#pragma unroll
+      for (int s = 0; s < KW; ++s)
+        if (ALL || ((am >> s) & 1u)) pacc[s] = M::mma(a, vf[s][c], pacc[s]);
+    }
+    Op po[KW][NC2];
+    Op dso[NPAIR][KW][NC2];
+#pragma unroll
+    for (int s = 0; s < KW; ++s) {
+      if (!(ALL || ((am >> s) & 1u))) continue;
+      float pv[16], d1[16], d2[16];
+      if (FULL || ((fm >> s) & 1u)) {
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const float r1 = sacc[0][s][r], r2 = sacc[NPAIR - 1][s][r];
+          pv[r] = poly_value<POLY>(r1, r2, p.kind, p.deg, p.sm, cf);
+          poly_grad<POLY, PAR>(r1, r2, pacc[s][r], p.kind, p.deg, p.sm, cf, d1[r], d2[r], gsum);
+        }
+      } else {
+        const int key = ka[s] + l32;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int qo = 32 * qb + key_off<T>(r, h);
+          const bool vis = key <= m + qo && dsl[qo] <= key;
+          const float r1 = sacc[0][s][r], r2 = sacc[NPAIR - 1][s][r];
+          pv[r] = vis ? poly_value<POLY>(r1, r2, p.kind, p.deg, p.sm, cf) : 0.f;
+          poly_grad<POLY, PAR>(r1, r2, vis ? pacc[s][r] : 0.f, p.kind, p.deg, p.sm, cf, d1[r], d2[r], gsum);
+        }
+      }
+#pragma unroll
+      for (int c2 = 0; c2 < NC2; ++c2) {
+        po[s][c2] = M::cvt(pv + c2 * EPL);
+        dso[0][s][c2] = M::cvt(d1 + c2 * EPL);
+        if constexpr (NPAIR == 2) dso[NPAIR - 1][s][c2] = M::cvt(d2 + c2 * EPL);
+      }
+    }
+#pragma unroll
+    for (int d = 0; d < NDV; ++d)
+#pragma unroll
+      for (int c2 = 0; c2 < NC2; ++c2) {
+        const Op a = read_col<T, OTile>(base + NPAIR * QTile::BYTES, 32 * qb + c2 * KC, 32 * d, lane);
+#pragma unroll
+        for (int s = 0; s < KW; ++s)
+          if (ALL || ((am >> s) & 1u)) dv[s][d] = M::mma(a, po[s][c2], dv[s][d]);
+      }
+#pragma unroll
+    for (int pr = 0; pr < NPAIR; ++pr)
+#pragma unroll
+      for (int d = 0; d < NDK; ++d)
+#pragma unroll
+        for (int c2 = 0; c2 < NC2; ++c2) {
+          const Op a = read_col<T, QTile>(base + pr * QTile::BYTES, 32 * qb + c2 * KC, 32 * d, lane);
+#pragma unroll
+          for (int s = 0; s < KW; ++s)
+            if (ALL || ((am >> s) & 1u)) dk[pr][s][d] = M::mma(a, dso[pr][s][c2], dk[pr][s][d]);
+        }
+  };
+
+  auto step = [&](const int m, auto fast_c) {
+    constexpr bool FAST = decltype(fast_c)::value;
     const bool more = m + BMQ < qhi;
     if (more) {
 #pragma unroll
@@ -569,89 +725,27 @@ __global__ void __launch_bounds__(NW * 64) k_bwd_kv(const KParams p) {
     }
     const char TNPA_LDS* base = smem + cur * BUF;
     const int TNPA_LDS* dsl = (const int TNPA_LDS*)(base + DSOFF);
+    if constexpr (FAST) {
 #pragma unroll
-    for (int qb = 0; qb < NQB; ++qb) {
-      const int q0 = m + 32 * qb;
-      if (q0 >= T_) continue;
-      const int qlast = min(q0 + 31, T_ - 1);
-      const int ds0 = dsl[32 * qb], dsL = dsl[qlast - m];
-      bool act[KW];
-      bool any = false;
+      for (int qb = 0; qb < NQB; ++qb) sub(base, dsl, m, qb, 0u, 0u, std::true_type{}, std::true_type{});
+    } else {
 #pragma unroll
-      for (int s = 0; s < KW; ++s) {
-        act[s] = ka[s] < T_ && ka[s] <= qlast && ka[s] + 31 >= ds0;
-        any |= act[s];
-      }
-      if (!any) continue;
-      f32x16 sacc[NPAIR][KW], pacc[KW];
+      for (int qb = 0; qb < NQB; ++qb) {
+        const int q0 = m + 32 * qb;
+        if (q0 >= T_) continue;
+        const int qlast = min(q0 + 31, T_ - 1);
+        const int ds0 = dsl[32 * qb], dsL = dsl[qlast - m];
+        uint32_t am = 0, fm = 0;
 #pragma unroll
-      for (int s = 0; s < KW; ++s) {
-        pacc[s] = zero16();
-#pragma unroll
-        for (int pr = 0; pr < NPAIR; ++pr) sacc[pr][s] = zero16();
-      }
-      const int qrow = 32 * qb + kappa<T>(l32);
-#pragma unroll
-      for (int c = 0; c < NCK; ++c)
-#pragma unroll
-        for (int pr = 0; pr < NPAIR; ++pr) {
-          const Op a = read_row<T, QTile>(base + pr * QTile::BYTES, qrow, c, h);
-#pragma unroll
-          for (int s = 0; s < KW; ++s)
-            if (act[s]) sacc[pr][s] = M::mma(a, kf[pr][s][c], sacc[pr][s]);
+        for (int s = 0; s < KW; ++s) {
+          if (ka[s] < T_ && ka[s] <= qlast && ka[s] + 31 >= ds0) am |= 1u << s;
+          if (ka[s] + 31 <= q0 && dsL <= ka[s] && q0 + 31 < T_) fm |= 1u << s;
         }
-#pragma unroll
-      for (int c = 0; c < NCV; ++c) {
-        const Op a = read_row<T, OTile>(base + NPAIR * QTile::BYTES, qrow, c, h);
-#pragma unroll
-        for (int s = 0; s < KW; ++s)
-          if (act[s]) pacc[s] = M::mma(a, vf[s][c], pacc[s]);
+        am = __builtin_amdgcn_readfirstlane(am);
+        fm = __builtin_amdgcn_readfirstlane(fm);
+        if (am == 0) continue;
+        sub(base, dsl, m, qb, am, fm, std::false_type{}, std::false_type{});
       }
-      Op po[KW][NC2];
-      Op dso[NPAIR][KW][NC2];
-#pragma unroll
-      for (int s = 0; s < KW; ++s) {
-        if (!act[s]) continue;
-        const bool full = ka[s] + 31 <= q0 && dsL <= ka[s] && q0 + 31 < T_;
-        const int key = ka[s] + l32;
-        float pv[16], d1[16], d2[16];
-#pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          const int qo = 32 * qb + key_off<T>(r, h);
-          bool vis = true;
-          if (!full) vis = key <= m + qo && dsl[qo] <= key;
-          const float r1 = sacc[0][s][r], r2 = sacc[NPAIR - 1][s][r];
-          pv[r] = vis ? poly_value<POLY>(r1, r2, p.kind, p.deg, p.sm, cf) : 0.f;
-          const float hg = vis ? pacc[s][r] : 0.f;
-          poly_grad<POLY, PAR>(r1, r2, hg, p.kind, p.deg, p.sm, cf, d1[r], d2[r], gsum);
-        }
-#pragma unroll
-        for (int c2 = 0; c2 < NC2; ++c2) {
-          po[s][c2] = M::cvt(pv + c2 * EPL);
-          dso[0][s][c2] = M::cvt(d1 + c2 * EPL);
-          if constexpr (NPAIR == 2) dso[NPAIR - 1][s][c2] = M::cvt(d2 + c2 * EPL);
-        }
-      }
-#pragma unroll
-      for (int d = 0; d < NDV; ++d)
-#pragma unroll
-        for (int c2 = 0; c2 < NC2; ++c2) {
-          const Op a = read_col<T, OTile>(base + NPAIR * QTile::BYTES, 32 * qb + c2 * KC, 32 * d, lane);
-#pragma unroll
-          for (int s = 0; s < KW; ++s)
-            if (act[s]) dv[s][d] = M::mma(a, po[s][c2], dv[s][d]);
-        }
-#pragma unroll
-      for (int pr = 0; pr < NPAIR; ++pr)
-#pragma unroll
-        for (int d = 0; d < NDK; ++d)
-#pragma unroll
-          for (int c2 = 0; c2 < NC2; ++c2) {
-            const Op a = read_col<T, QTile>(base + pr * QTile::BYTES, 32 * qb + c2 * KC, 32 * d, lane);
-#pragma unroll
-            for (int s = 0; s < KW; ++s)
-              if (act[s]) dk[pr][s][d] = M::mma(a, dso[pr][s][c2], dk[pr][s][d]);
-          }
     }
     if (more) {
       char TNPA_LDS* nxt = smem + (cur ^ 1) * BUF;
@@ -662,7 +756,23 @@ __global__ void __launch_bounds__(NW * 64) k_bwd_kv(const KParams p) {
     }
     __syncthreads();
     cur ^= 1;
+  };
+  // Query tiles qlo, qlo+BMQ, ... < qhi, split per wave into: the diagonal (generic), tiles whose every query sees
+  // every key of the wave (fast), and tiles past the wave's document end or the sequence end (generic).
+  const int ntile = (qhi - qlo + BMQ - 1) / BMQ;
+  int j0 = ntile, j1 = ntile;
+  if (nw0 < T_) {
+    const int klast = nw0 + 32 * KW - 1;
+    const int qe = min(T_, p.qend[(int64_t)b * T_ + nw0]);
+    j0 = min(ntile, max(0, (klast - qlo + BMQ - 1) / BMQ));
+    j1 = max(j0, min(ntile, (qe - qlo) / BMQ));
   }
+  j0 = __builtin_amdgcn_readfirstlane(j0);
+  j1 = __builtin_amdgcn_readfirstlane(j1);
+  int j = 0;
+  for (; j < j0; ++j) step(qlo + j * BMQ, std::false_type{});
+  for (; j < j1; ++j) step(qlo + j * BMQ, std::true_type{});
+  for (; j < ntile; ++j) step(qlo + j * BMQ, std::false_type{});
 
   const TDesc* kouts[2] = {&p.dk1, &p.dk2};
 #pragma unroll
@@ -723,7 +833,7 @@ template <typename T, int POLY, int DK, int DV> hipError_t launch_fwd(const KPar
   typedef Cfg<T, POLY, DK, DV> C;
   constexpr int BM = C::FW_NW * C::FW_QW * 32;
   const int grid = p.B * p.H * ((p.T + BM - 1) / BM);
-  hipLaunchKernelGGL((k_fwd<T, POLY, DK, DV, C::FW_NW, C::FW_QW, C::FW_BN>), dim3(grid), dim3(C::FW_NW * 64), 0, st, p);
+  hipLaunchKernelGGL((k_fwd<T, POLY, DK, DV, C::FW_NW, C::FW_QW, C::FW_BN, C::FW_WPE>), dim3(grid), dim3(C::FW_NW * 64), 0, st, p);
   return hipGetLastError();
 }
 
@@ -731,7 +841,7 @@ template <typename T, int POLY, int DK, int DV> hipError_t launch_bwd_kv(const K
   typedef Cfg<T, POLY, DK, DV> C;
   static_assert(C::KV_KEYS == KV_BLOCK_KEYS, "dK/dV block size is fixed");
   const int grid = p.B * p.H * ((p.T + C::KV_KEYS - 1) / C::KV_KEYS);
-  hipLaunchKernelGGL((k_bwd_kv<T, POLY, DK, DV, C::KV_NW, C::KV_KW, C::KV_BM>), dim3(grid), dim3(C::KV_NW * 64), 0, st,
+  hipLaunchKernelGGL((k_bwd_kv<T, POLY, DK, DV, C::KV_NW, C::KV_KW, C::KV_BM, C::KV_WPE>), dim3(grid), dim3(C::KV_NW * 64), 0, st,
                      p);
   return hipGetLastError();
 }
@@ -740,7 +850,7 @@ template <typename T, int POLY, int DK, int DV> hipError_t launch_bwd_q(const KP
   typedef Cfg<T, POLY, DK, DV> C;
   constexpr int BM = C::BQ_NW * C::BQ_QW * 32;
   const int grid = p.B * p.H * ((p.T + BM - 1) / BM);
-  hipLaunchKernelGGL((k_bwd_q<T, POLY, DK, DV, C::BQ_NW, C::BQ_QW, C::BQ_BN>), dim3(grid), dim3(C::BQ_NW * 64), 0, st,
+  hipLaunchKernelGGL((k_bwd_q<T, POLY, DK, DV, C::BQ_NW, C::BQ_QW, C::BQ_BN, C::BQ_WPE>), dim3(grid), dim3(C::BQ_NW * 64), 0, st,
                      p);
   return hipGetLastError();
 }
