@@ -88,6 +88,21 @@ def kernel_times(q, k, v, do, doc, rs, degree, reps):
     return out
 
 
+def measured_traffic(config, kernel):
+    """HBM bytes per launch of `kernel` from the committed rocprofv3 FETCH_SIZE / WRITE_SIZE summary
+    (profiles/hbm_traffic_<config>.txt, counters scaled by a plain-copy calibration), or None if not profiled."""
+    path = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles", f"hbm_traffic_{config}.txt")
+    try:
+        with open(path) as f:
+            for line in f:
+                parts = line.split()
+                if len(parts) == 4 and parts[0] == "k_" + kernel:
+                    return int(parts[3])
+    except OSError:
+        pass
+    return None
+
+
 def cpu_baseline(B, H, T, D, degree, seconds):
     """Times the CPU oracle (float32 numpy dense restatement) fwd+bwd over (b, h) slices until `seconds` pass."""
     import numpy as np
@@ -126,6 +141,9 @@ def main(argv=None):
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--kernel-reps", type=int, default=20)
+    ap.add_argument("--copy-probe-mib", type=int, default=0,
+                    help="only run a plain device-to-device copy of this many MiB (3 times) and exit: the known-size "
+                         "kernel that calibrates rocprofv3's FETCH_SIZE / WRITE_SIZE counters")
     a = ap.parse_args(argv)
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if a.gpus != 1 or world != 1:
@@ -135,10 +153,19 @@ def main(argv=None):
         return 2
 
     import torch
-    from tensor_train_ing_amd import poly_attention_hip
-    B, H, T, D, degree, boost, seed = CONFIGS[a.config]
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
+    if a.copy_probe_mib:
+        src = torch.ones(a.copy_probe_mib << 18, dtype=torch.float32, device=dev)
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        print(json.dumps({"copy_probe_bytes": src.numel() * 4, "dispatches": 3}), flush=True)
+        return 0
+
+    from tensor_train_ing_amd import poly_attention_hip
+    B, H, T, D, degree, boost, seed = CONFIGS[a.config]
     q, k, v, do, doc, rs = make_inputs(B, H, T, D, boost, seed, dev)
     q.requires_grad_(); k.requires_grad_(); v.requires_grad_()  # noqa: E702
 
@@ -148,7 +175,7 @@ def main(argv=None):
 
     for _ in range(a.warmup):
         step()
-    torch.cuda.synchronize()
+    torch.cuda.synchronize()  # one process, one GPU: the synchronize is the whole barrier
     t0 = time.perf_counter()
     ms_ev = time_events(step, a.steps)
     torch.cuda.synchronize()
@@ -176,7 +203,8 @@ def main(argv=None):
         "wall_ms_per_step": round(wall_ms, 4),
         "kernel_ms": {n: round(t, 4) for n, t in kt.items()},
         "roofline": {"bound": "mfma", "kernel": dom, "achieved": round(ach, 2), "peak": PEAK_TFLOPS,
-                     "unit": "TFLOP/s", "frac": round(ach / PEAK_TFLOPS, 4), "traffic": None},
+                     "unit": "TFLOP/s", "frac": round(ach / PEAK_TFLOPS, 4),
+                     "traffic": measured_traffic(a.config, dom)},
     }
     if not a.no_cpu_baseline:
         line["cpu_baseline"] = cpu_baseline(B, H, T, D, degree, a.cpu_seconds)
