@@ -73,7 +73,8 @@ def kernel_times(q, k, v, do, doc, rs, degree, reps):
     prob = _problem(_abi.POWER, degree, q, k, q, k, v, dstart, qend, rs, None, None)
     o = torch.empty_like(v)
     dq, dk, dv = torch.empty_like(q), torch.empty_like(k), torch.empty_like(v)
-    grads = _abi.Grads(_desc(do), _desc(dq), _desc(dk), _desc(dq), _desc(dk), _desc(dv), None, None)
+    dos = torch.empty_like(do)  # row-scaled dO workspace, as the operator passes it
+    grads = _abi.Grads(_desc(do), _desc(dq), _desc(dk), _desc(dq), _desc(dk), _desc(dv), None, None, _desc(dos))
     st = _stream(q.device)
     od = _desc(o)
     fwd = lambda: _abi.check(lib.tnpa_forward(ctypes.byref(prob), ctypes.byref(od), st), "fwd")  # noqa: E731

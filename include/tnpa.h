@@ -24,7 +24,7 @@
 extern "C" {
 #endif
 
-#define TNPA_ABI_VERSION 1
+#define TNPA_ABI_VERSION 2
 
 typedef enum {
   TNPA_OK = 0,
@@ -66,11 +66,16 @@ typedef struct {
 /* Gradients for tnpa_backward. dout is dL/dy (B,H,T,dv). dq2/dk2 are ignored for one-pair kinds. dpar_partial is
  * a caller-allocated fp32 workspace of tnpa_dpar_workspace_floats() floats, and dpar an (H,4) fp32 output
  * (column 0 = db for offset_square, the 4 columns = dcoef for lower_degree_mix); both may be NULL for
- * signed_product / power, and are required for the other two kinds. */
+ * signed_product / power, and are required for the other two kinds.
+ * dout_scaled is an optional caller-allocated workspace (B,H,T,dv) in the problem dtype: when its data is not NULL
+ * the dK/dV pass first writes row_scale[b,t] * dout[b,h,t,:] into it (computed in fp32, rounded to the dtype,
+ * exactly as the pass would round it on the fly) and then streams it instead of rescaling dout per tile. It has no
+ * counterpart in the reference (whose Triton kernel scales in registers). */
 typedef struct {
   tnpa_tensor_t dout, dq1, dk1, dq2, dk2, dv;
   float* dpar_partial;
   float* dpar;
+  tnpa_tensor_t dout_scaled;
 } tnpa_grads_t;
 
 /* Library ABI version (TNPA_ABI_VERSION). */

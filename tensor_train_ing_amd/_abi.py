@@ -10,7 +10,7 @@ import os
 from pathlib import Path
 
 LIB_PATH = Path(__file__).resolve().parent / "libtnpa.so"
-ABI_VERSION = 1
+ABI_VERSION = 2
 
 OK, ERR_INVALID, ERR_UNSUPPORTED, ERR_LAUNCH = 0, 1, 2, 3
 BF16, F32, F16 = 0, 1, 2
@@ -36,7 +36,8 @@ class Problem(ctypes.Structure):
 class Grads(ctypes.Structure):
     """tnpa_grads_t"""
     _fields_ = [("dout", Tensor), ("dq1", Tensor), ("dk1", Tensor), ("dq2", Tensor), ("dk2", Tensor),
-                ("dv", Tensor), ("dpar_partial", ctypes.c_void_p), ("dpar", ctypes.c_void_p)]
+                ("dv", Tensor), ("dpar_partial", ctypes.c_void_p), ("dpar", ctypes.c_void_p),
+                ("dout_scaled", Tensor)]
 
 
 _SIGNATURES = {

@@ -1,5 +1,6 @@
 // C ABI of libtnpa.so: argument validation, dtype/kind/head-dim dispatch to the kernel instantiations, the
 // document-bounds prepass and the fixed-order dcoef/db reduction.  Declared in include/tnpa.h.
+#include <algorithm>
 #include <cmath>
 #include <cstdarg>
 #include <cstdio>
@@ -198,6 +199,48 @@ __global__ void __launch_bounds__(256) k_doc_bounds(const void* doc, int is64, i
   }
 }
 
+// out[b,h,t,:] = row_scale[b,t] * dout[b,h,t,:], one 16-byte chunk per thread (grid-stride), computed in fp32 and
+// rounded to T exactly as the dK/dV pass rounds it when it scales dout while staging.
+template <typename T>
+__global__ void __launch_bounds__(256) k_scale_rows(const T* __restrict__ dout, int64_t sb, int64_t sh, int64_t st,
+                                                    const float* __restrict__ rs, int B, int H, int T_, int D,
+                                                    T* __restrict__ out, int64_t ob, int64_t oh, int64_t ot) {
+  constexpr int CE = 16 / (int)sizeof(T);
+  const int nch = D / CE;
+  const int64_t total = (int64_t)B * H * T_ * nch;
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total; i += (int64_t)gridDim.x * blockDim.x) {
+    const int c = (int)(i % nch);
+    const int64_t row = i / nch;
+    const int t = (int)(row % T_);
+    const int64_t bh = row / T_;
+    const int h = (int)(bh % H), b = (int)(bh / H);
+    const float f = rs[(int64_t)b * T_ + t];
+    typedef unsigned int u4 __attribute__((ext_vector_type(4)));
+    u4 raw = *(const u4*)(dout + b * sb + h * sh + t * st + c * CE);
+    if constexpr (sizeof(T) == 2) {
+      T* e = reinterpret_cast<T*>(&raw);
+#pragma unroll
+      for (int j = 0; j < 8; ++j) e[j] = (T)((float)e[j] * f);
+    } else {
+      float* e = reinterpret_cast<float*>(&raw);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) e[j] *= f;
+    }
+    *(u4*)(out + b * ob + h * oh + t * ot + c * CE) = raw;
+  }
+}
+
+template <typename T>
+hipError_t scale_rows(const tnpa_problem_t& p, const tnpa_tensor_t& d, const tnpa_tensor_t& o, hipStream_t s) {
+  const int CE = 16 / (int)sizeof(T);
+  const int64_t total = (int64_t)p.batch * p.heads * p.seq_len * (p.head_dim_v / CE);
+  const int grid = (int)std::min<int64_t>((total + 255) / 256, 8192);
+  hipLaunchKernelGGL(k_scale_rows<T>, dim3(grid), dim3(256), 0, s, (const T*)d.data, d.stride_b, d.stride_h,
+                     d.stride_t, p.row_scale, p.batch, p.heads, p.seq_len, p.head_dim_v, (T*)o.data, o.stride_b,
+                     o.stride_h, o.stride_t);
+  return hipGetLastError();
+}
+
 // dpar[h, c] = sum over (b, key block) of the per-block partials, in a fixed order.
 // ref: tnlm/kernels/poly_attn.py:304 (dpar.view(B, H, NB, 4).sum((0, 2)))
 __global__ void k_dpar_reduce(const float* part, int B, int H, int NNB, float* out) {
@@ -284,6 +327,18 @@ int tnpa_backward_phase(const tnpa_problem_t* problem, const tnpa_grads_t* grads
   }
   k.dpar = par ? grads->dpar_partial : nullptr;
   hipError_t e;
+  const bool pre = kv && grads->dout_scaled.data != nullptr;
+  if (pre) {
+    if ((rc = check_tensor(grads->dout_scaled, "dout_scaled", p, es))) return rc;
+    switch (p.dtype) {
+      case TNPA_BF16: e = scale_rows<__bf16>(p, grads->dout, grads->dout_scaled, (hipStream_t)stream); break;
+      case TNPA_F16: e = scale_rows<_Float16>(p, grads->dout, grads->dout_scaled, (hipStream_t)stream); break;
+      default: e = scale_rows<float>(p, grads->dout, grads->dout_scaled, (hipStream_t)stream); break;
+    }
+    if (e != hipSuccess) return fail(TNPA_ERR_LAUNCH, "tnpa_backward (row scaling): %s", hipGetErrorString(e));
+    k.dsc = desc(grads->dout_scaled);
+    k.dpre = 1;
+  }
   if (kv) {
     e = run(PH_BWD_KV, p, k, (hipStream_t)stream);
     if (e != hipSuccess) return fail(TNPA_ERR_LAUNCH, "tnpa_backward (dK/dV): %s", hipGetErrorString(e));

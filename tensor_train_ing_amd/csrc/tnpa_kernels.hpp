@@ -116,6 +116,7 @@ template <typename T, int POLY, int DK, int DV> struct Cfg {
   static constexpr int FW_NW = 4, FW_QW = 1, FW_BN = F32 ? 32 : 64, FW_WPE = (F32 || NPAIR == 2) ? 1 : 2;
   static constexpr int BQ_NW = 4, BQ_QW = 1, BQ_BN = F32 ? 32 : 64, BQ_WPE = (F32 || NPAIR == 2) ? 1 : 2;
   static constexpr int KV_NW = 4, KV_KW = 1, KV_BM = F32 ? 32 : 64, KV_WPE = 1;
+  static constexpr bool KV_SPLIT = !F32 && NPAIR == 1;  // separate dV and dK passes at two waves per SIMD
   static constexpr int KV_KEYS = KV_NW * KV_KW * 32;
 };
 
@@ -549,14 +550,19 @@ k_bwd_q(const KParams p) {
 
 // ------------------------------------------------------------------------------------------------ dK / dV
 // ref: tnlm/kernels/poly_attn.py:77-148 (_bwd_kv)
-template <typename T, int POLY, int DK, int DV, int NW, int KW, int BMQ, int WPE>
+// MODE: KV_BOTH computes dK and dV in one pass (one wave per SIMD: dK, dV, K and V all stay in registers);
+// KV_DV and KV_DK split them into two passes that each fit two waves per SIMD (the S = Q K^T product is computed
+// in both passes).
+enum { KV_BOTH = 0, KV_DV = 1, KV_DK = 2 };
+template <typename T, int POLY, int DK, int DV, int NW, int KW, int BMQ, int WPE, int MODE>
 __global__ void __attribute__((amdgpu_flat_work_group_size(NW * 64, NW * 64), amdgpu_waves_per_eu(WPE)))
 k_bwd_kv(const KParams p) {
   typedef Mfma<T> M;
   typedef typename M::Op Op;
   constexpr int KC = M::KC, EPL = M::EPL, NT = NW * 64;
   constexpr int NPAIR = POLY == POLY_GEN2 ? 2 : 1;
-  constexpr bool PAR = POLY != POLY_POW2;
+  constexpr bool PAR = POLY != POLY_POW2 && MODE != KV_DV;
+  constexpr bool WANT_DV = MODE != KV_DK, WANT_DK = MODE != KV_DV;
   constexpr int DKP = DK < 32 ? 32 : DK, DVP = DV < 32 ? 32 : DV;
   constexpr int NCK = DK / KC, NCV = DV / KC, NDK = DKP / 32, NDV = DVP / 32, NQB = BMQ / 32, NC2 = 32 / KC;
   constexpr int BNK = NW * KW * 32;
@@ -624,7 +630,9 @@ k_bwd_kv(const KParams p) {
   constexpr int DSOFF = NPAIR * QTile::BYTES + OTile::BYTES;
 #pragma unroll
   for (int pr = 0; pr < NPAIR; ++pr) sq[pr].load(qp[pr], qst[pr], qlo, T_ - qlo);
-  so.load_scaled(dop, p.dout.st, qlo, T_ - qlo, rsc);
+  const T* dscp = head_ptr<T>(p.dsc, b, hd);
+  if (p.dpre) so.load(dscp, p.dsc.st, qlo, T_ - qlo);
+  else so.load_scaled(dop, p.dout.st, qlo, T_ - qlo, rsc);
   int dsv = 0;
   if (threadIdx.x < BMQ) dsv = qlo + (int)threadIdx.x < T_ ? dst[qlo + threadIdx.x] : INT_MAX;
 #pragma unroll
@@ -654,12 +662,14 @@ k_bwd_kv(const KParams p) {
         for (int s = 0; s < KW; ++s)
           if (ALL || ((am >> s) & 1u)) sacc[pr][s] = M::mma(a, kf[pr][s][c], sacc[pr][s]);
       }
+    if constexpr (WANT_DK) {
 #pragma unroll
-    for (int c = 0; c < NCV; ++c) {
-      const Op a = read_row<T, OTile>(base + NPAIR * QTile::BYTES, 32 * qb, kappa<T>(l32), c, h);
+      for (int c = 0; c < NCV; ++c) {
+        const Op a = read_row<T, OTile>(base + NPAIR * QTile::BYTES, 32 * qb, kappa<T>(l32), c, h);
 #pragma unroll
-      for (int s = 0; s < KW; ++s)
-        if (ALL || ((am >> s) & 1u)) pacc[s] = M::mma(a, vf[s][c], pacc[s]);
+        for (int s = 0; s < KW; ++s)
+          if (ALL || ((am >> s) & 1u)) pacc[s] = M::mma(a, vf[s][c], pacc[s]);
+      }
     }
     Op po[KW][NC2];
     Op dso[NPAIR][KW][NC2];
@@ -671,8 +681,8 @@ k_bwd_kv(const KParams p) {
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
           const float r1 = sacc[0][s][r], r2 = sacc[NPAIR - 1][s][r];
-          pv[r] = poly_value<POLY>(r1, r2, p.kind, p.deg, p.sm, cf);
-          poly_grad<POLY, PAR>(r1, r2, pacc[s][r], p.kind, p.deg, p.sm, cf, d1[r], d2[r], gsum);
+          if constexpr (WANT_DV) pv[r] = poly_value<POLY>(r1, r2, p.kind, p.deg, p.sm, cf);
+          if constexpr (WANT_DK) poly_grad<POLY, PAR>(r1, r2, pacc[s][r], p.kind, p.deg, p.sm, cf, d1[r], d2[r], gsum);
         }
       } else {
         const int key = ka[s] + l32;
@@ -681,37 +691,44 @@ k_bwd_kv(const KParams p) {
           const int qo = 32 * qb + key_off<T>(r, h);
           const bool vis = key <= m + qo && dsl[qo] <= key;
           const float r1 = sacc[0][s][r], r2 = sacc[NPAIR - 1][s][r];
-          pv[r] = vis ? poly_value<POLY>(r1, r2, p.kind, p.deg, p.sm, cf) : 0.f;
-          poly_grad<POLY, PAR>(r1, r2, vis ? pacc[s][r] : 0.f, p.kind, p.deg, p.sm, cf, d1[r], d2[r], gsum);
+          if constexpr (WANT_DV) pv[r] = vis ? poly_value<POLY>(r1, r2, p.kind, p.deg, p.sm, cf) : 0.f;
+          if constexpr (WANT_DK)
+            poly_grad<POLY, PAR>(r1, r2, vis ? pacc[s][r] : 0.f, p.kind, p.deg, p.sm, cf, d1[r], d2[r], gsum);
         }
       }
 #pragma unroll
       for (int c2 = 0; c2 < NC2; ++c2) {
-        po[s][c2] = M::cvt(pv + c2 * EPL);
-        dso[0][s][c2] = M::cvt(d1 + c2 * EPL);
-        if constexpr (NPAIR == 2) dso[NPAIR - 1][s][c2] = M::cvt(d2 + c2 * EPL);
+        if constexpr (WANT_DV) po[s][c2] = M::cvt(pv + c2 * EPL);
+        if constexpr (WANT_DK) {
+          dso[0][s][c2] = M::cvt(d1 + c2 * EPL);
+          if constexpr (NPAIR == 2) dso[NPAIR - 1][s][c2] = M::cvt(d2 + c2 * EPL);
+        }
       }
     }
+    if constexpr (WANT_DV) {
 #pragma unroll
-    for (int d = 0; d < NDV; ++d)
-#pragma unroll
-      for (int c2 = 0; c2 < NC2; ++c2) {
-        const Op a = read_col<T, OTile>(base + NPAIR * QTile::BYTES, 32 * qb + c2 * KC, 32 * d, lane);
-#pragma unroll
-        for (int s = 0; s < KW; ++s)
-          if (ALL || ((am >> s) & 1u)) dv[s][d] = M::mma(a, po[s][c2], dv[s][d]);
-      }
-#pragma unroll
-    for (int pr = 0; pr < NPAIR; ++pr)
-#pragma unroll
-      for (int d = 0; d < NDK; ++d)
+      for (int d = 0; d < NDV; ++d)
 #pragma unroll
         for (int c2 = 0; c2 < NC2; ++c2) {
-          const Op a = read_col<T, QTile>(base + pr * QTile::BYTES, 32 * qb + c2 * KC, 32 * d, lane);
+          const Op a = read_col<T, OTile>(base + NPAIR * QTile::BYTES, 32 * qb + c2 * KC, 32 * d, lane);
 #pragma unroll
           for (int s = 0; s < KW; ++s)
-            if (ALL || ((am >> s) & 1u)) dk[pr][s][d] = M::mma(a, dso[pr][s][c2], dk[pr][s][d]);
+            if (ALL || ((am >> s) & 1u)) dv[s][d] = M::mma(a, po[s][c2], dv[s][d]);
         }
+    }
+    if constexpr (WANT_DK) {
+#pragma unroll
+      for (int pr = 0; pr < NPAIR; ++pr)
+#pragma unroll
+        for (int d = 0; d < NDK; ++d)
+#pragma unroll
+          for (int c2 = 0; c2 < NC2; ++c2) {
+            const Op a = read_col<T, QTile>(base + pr * QTile::BYTES, 32 * qb + c2 * KC, 32 * d, lane);
+#pragma unroll
+            for (int s = 0; s < KW; ++s)
+              if (ALL || ((am >> s) & 1u)) dk[pr][s][d] = M::mma(a, dso[pr][s][c2], dk[pr][s][d]);
+          }
+    }
   };
 
   auto step = [&](const int m, auto fast_c) {
@@ -720,7 +737,8 @@ k_bwd_kv(const KParams p) {
     if (more) {
 #pragma unroll
       for (int pr = 0; pr < NPAIR; ++pr) sq[pr].load(qp[pr], qst[pr], m + BMQ, T_ - m - BMQ);
-      so.load_scaled(dop, p.dout.st, m + BMQ, T_ - m - BMQ, rsc);
+      if (p.dpre) so.load(dscp, p.dsc.st, m + BMQ, T_ - m - BMQ);
+      else so.load_scaled(dop, p.dout.st, m + BMQ, T_ - m - BMQ, rsc);
       if (threadIdx.x < BMQ) dsv = m + BMQ + (int)threadIdx.x < T_ ? dst[m + BMQ + threadIdx.x] : INT_MAX;
     }
     const char TNPA_LDS* base = smem + cur * BUF;
@@ -781,7 +799,7 @@ k_bwd_kv(const KParams p) {
     if (key >= T_) continue;
     T* vrow = head_ptr_w<T>(p.dv, b, hd) + (int64_t)key * p.dv.st;
 #pragma unroll
-    for (int d = 0; d < NDV; ++d)
+    for (int d = 0; d < (WANT_DV ? NDV : 0); ++d)
 #pragma unroll
       for (int g = 0; g < 4; ++g) {
         const int col = 32 * d + 8 * g + 4 * h;
@@ -790,7 +808,7 @@ k_bwd_kv(const KParams p) {
                     dv[s][d][4 * g + 3] * p.vf);
       }
 #pragma unroll
-    for (int pr = 0; pr < NPAIR; ++pr) {
+    for (int pr = 0; pr < (WANT_DK ? NPAIR : 0); ++pr) {
       T* krow = head_ptr_w<T>(*kouts[pr], b, hd) + (int64_t)key * kouts[pr]->st;
 #pragma unroll
       for (int d = 0; d < NDK; ++d)
@@ -841,8 +859,15 @@ template <typename T, int POLY, int DK, int DV> hipError_t launch_bwd_kv(const K
   typedef Cfg<T, POLY, DK, DV> C;
   static_assert(C::KV_KEYS == KV_BLOCK_KEYS, "dK/dV block size is fixed");
   const int grid = p.B * p.H * ((p.T + C::KV_KEYS - 1) / C::KV_KEYS);
-  hipLaunchKernelGGL((k_bwd_kv<T, POLY, DK, DV, C::KV_NW, C::KV_KW, C::KV_BM, C::KV_WPE>), dim3(grid), dim3(C::KV_NW * 64), 0, st,
-                     p);
+  if constexpr (C::KV_SPLIT) {
+    hipLaunchKernelGGL((k_bwd_kv<T, POLY, DK, DV, C::KV_NW, C::KV_KW, C::KV_BM, 2, KV_DV>), dim3(grid), dim3(C::KV_NW * 64),
+                       0, st, p);
+    hipLaunchKernelGGL((k_bwd_kv<T, POLY, DK, DV, C::KV_NW, C::KV_KW, C::KV_BM, 2, KV_DK>), dim3(grid), dim3(C::KV_NW * 64),
+                       0, st, p);
+  } else {
+    hipLaunchKernelGGL((k_bwd_kv<T, POLY, DK, DV, C::KV_NW, C::KV_KW, C::KV_BM, C::KV_WPE, KV_BOTH>), dim3(grid),
+                       dim3(C::KV_NW * 64), 0, st, p);
+  }
   return hipGetLastError();
 }
 

@@ -20,12 +20,14 @@ struct TDesc {
 struct KParams {
   TDesc q1, k1, q2, k2, v, o;
   TDesc dout, dq1, dk1, dq2, dk2, dv;
+  TDesc dsc;           // row_scale * dout (same shape), read by the dK/dV pass when dpre != 0
   const int* dstart;   // (B, T) first visible key of each query (q + 1 for padding)
   const int* qend;     // (B, T) one past the last query that sees each key
   const float* rscale; // (B, T) row scale n_visible^-p (0 for padding)
   const float* coef;   // (H, 4) lower_degree_mix coefficients or null
   const float* offs;   // (H) offset_square offsets or null
   float* dpar;         // (B*H, NNB, 4) per-key-block partial sums for dcoef / db, or null
+  int dpre;            // 1: dsc holds the row-scaled dout; 0: the dK/dV pass scales dout while staging it
   int B, H, T;
   int kind, deg;
   float sm;  // 1/sqrt(dk)

@@ -32,7 +32,7 @@ def _declared_functions():
 
 def test_library_loads_and_reports_abi_version(lib):
     from tensor_train_ing_amd import _abi
-    assert lib.tnpa_abi_version() == _abi.ABI_VERSION == 1
+    assert lib.tnpa_abi_version() == _abi.ABI_VERSION == 2
 
 
 def test_every_declared_symbol_is_exported(lib):
@@ -56,7 +56,8 @@ int main(void) {
   printf("%zu %zu %zu\n", sizeof(tnpa_tensor_t), sizeof(tnpa_problem_t), sizeof(tnpa_grads_t));
   printf("%zu %zu %zu %zu\n", offsetof(tnpa_problem_t, q1), offsetof(tnpa_problem_t, v),
          offsetof(tnpa_problem_t, doc_start), offsetof(tnpa_problem_t, offset));
-  printf("%zu %zu\n", offsetof(tnpa_grads_t, dv), offsetof(tnpa_grads_t, dpar));
+  printf("%zu %zu %zu\n", offsetof(tnpa_grads_t, dv), offsetof(tnpa_grads_t, dpar),
+         offsetof(tnpa_grads_t, dout_scaled));
   return 0;
 }''')
     exe = tmp_path / "layout"
@@ -67,7 +68,7 @@ int main(void) {
     P, G = _abi.Problem, _abi.Grads
     assert got[0] == [ctypes.sizeof(_abi.Tensor), ctypes.sizeof(P), ctypes.sizeof(G)]
     assert got[1] == [P.q1.offset, P.v.offset, P.doc_start.offset, P.offset.offset]
-    assert got[2] == [G.dv.offset, G.dpar.offset]
+    assert got[2] == [G.dv.offset, G.dpar.offset, G.dout_scaled.offset]
 
 
 def _problem(**kw):

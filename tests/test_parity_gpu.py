@@ -208,6 +208,96 @@ def test_deterministic_bitwise():
             assert torch.equal(r1[n], r2[n]), (kind, n)
 
 
+# ------------------------------------------------------------------ head dim 128, 16-bit: documents, padding, ragged T
+def _doc_rows(B, T):
+    """Documents of uneven lengths (some shorter than a 32-row sub-block, one starting on a 64-row tile edge),
+    plus trailing padding on the last row."""
+    docs = torch.zeros(B, T, dtype=torch.long)
+    for bi in range(B):
+        starts = [0, 7 + 13 * bi, 64, 64 + 29 * (bi + 1), T // 2 + 3]
+        for i, st in enumerate(sorted(set(min(x, T - 1) for x in starts))):
+            docs[bi, st:] = i
+    docs[-1, T - T // 7:] = -1
+    return docs
+
+
+@pytest.mark.parametrize("T", [64, 77, 300, 512])
+@pytest.mark.parametrize("docs", [False, True])
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_d128_power_degree2(T, docs, dtype):
+    B, H = 2, 3
+    d = _doc_rows(B, T) if docs else None
+    res, ref = _case("power", B, H, T, 128, 128, dtype, docs=d, degree=2, qk_scale=128 ** -0.25)
+    _check(compare(res, ref), BF16_FRO, BF16_MAX)
+
+
+@pytest.mark.parametrize("B,H,T", [(2, 4, 600), (1, 8, 1000), (3, 1, 850)])
+def test_d128_odd_block_counts(B, H, T):
+    """Odd and even numbers of 128-row query / key blocks, B*H a multiple of 8 and not, documents and padding."""
+    res, ref = _case("power", B, H, T, 128, 128, torch.bfloat16, docs=_doc_rows(B, T), degree=2,
+                     qk_scale=128 ** -0.25)
+    _check(compare(res, ref), BF16_FRO, BF16_MAX)
+
+
+@pytest.mark.parametrize("degree", [1, 3, 4])
+def test_d128_power_other_degrees(degree):
+    res, ref = _case("power", 2, 2, 333, 128, 128, torch.bfloat16, docs=_doc_rows(2, 333), degree=degree,
+                     qk_scale=128 ** -0.25)
+    _check(compare(res, ref), BF16_FRO, BF16_MAX)
+
+
+@pytest.mark.parametrize("T", [96, 260])
+def test_d128_offset_square(T):
+    res, ref = _case("offset_square", 2, 2, T, 128, 128, torch.bfloat16, docs=_doc_rows(2, T),
+                     qk_scale=128 ** -0.25)
+    _check(compare(res, ref), BF16_FRO, BF16_MAX)
+
+
+def test_d128_bthd_layout():
+    """(B, T, H, d) storage, the model's layout: time stride H*d, read in place."""
+    res, ref = _case("power", 2, 4, 200, 128, 128, torch.bfloat16, docs=_doc_rows(2, 200), degree=2,
+                     layout="bthd", qk_scale=128 ** -0.25)
+    _check(compare(res, ref), BF16_FRO, BF16_MAX)
+
+
+@pytest.mark.parametrize("kind,dtype", [("power", torch.bfloat16), ("offset_square", torch.float16),
+                                        ("lower_degree_mix", torch.bfloat16), ("power", torch.float32)])
+def test_prescaled_dout_matches_in_pass_scaling(kind, dtype):
+    """The dK/dV pass streaming the library-written row_scale * dO workspace gives bit-identical gradients to the
+    pass that scales dO while staging it (both round the product to the input dtype)."""
+    import ctypes
+    from tensor_train_ing_amd import _abi
+    from tensor_train_ing_amd.poly_attn import KINDS, _desc, _problem, _stream, doc_bounds
+    B, H, T, D = 2, 3, 300, 128 if dtype != torch.float32 else 64
+    two = kind in ("signed_product", "lower_degree_mix")
+    q1, k1, q2, k2, v, dout = (None if x is None else x.cuda()
+                               for x in gaussian_inputs(B, H, T, D, D, dtype, 11, qk_scale=D ** -0.25, two_pairs=two))
+    docs = _doc_rows(B, T).cuda()
+    rs = row_scale(docs, 0.5)
+    coef, bb = _params(H)
+    dstart, qend = doc_bounds(docs)
+    K = KINDS[kind]
+    prob = _problem(K, 2, q1, k1, q2 if two else q1, k2 if two else k1, v, dstart, qend, rs.float().contiguous(),
+                    coef.float().contiguous() if kind == "lower_degree_mix" else None,
+                    bb.float().contiguous() if kind == "offset_square" else None)
+    lib = _abi.load()
+    outs = []
+    for pre in (False, True):
+        dk1, dv, dk2 = torch.empty_like(k1), torch.empty_like(v), torch.empty_like(k1)
+        ws = torch.empty(max(1, lib.tnpa_dpar_workspace_floats(ctypes.byref(prob))), device="cuda")
+        dpar = torch.empty(H, 4, device="cuda")
+        dos = torch.empty_like(dout)
+        g = _abi.Grads(_desc(dout), _abi.Tensor(), _desc(dk1), _abi.Tensor(), _desc(dk2), _desc(dv),
+                       ws.data_ptr(), dpar.data_ptr(), _desc(dos) if pre else _abi.Tensor())
+        _abi.check(lib.tnpa_backward_phase(ctypes.byref(prob), ctypes.byref(g), _abi.PHASE_KV, _stream(q1.device)),
+                   "kv")
+        torch.cuda.synchronize()
+        outs.append((dk1, dv, dk2 if two else None, dpar if kind in ("offset_square", "lower_degree_mix") else None))
+    for a, b2 in zip(*outs):
+        if a is not None:
+            assert torch.equal(a, b2)
+
+
 # ------------------------------------------------------------------ BASELINE.json configurations, full size
 BASELINE_CONFIGS = {
     "100m_b16h12t1024d64_p2": dict(B=16, H=12, T=1024, D=64, degree=2, boost=0.0),
