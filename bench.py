@@ -77,11 +77,13 @@ def kernel_times(q, k, v, do, doc, rs, degree, reps):
     grads = _abi.Grads(_desc(do), _desc(dq), _desc(dk), _desc(dq), _desc(dk), _desc(dv), None, None, _desc(dos))
     st = _stream(q.device)
     od = _desc(o)
+    def phase(ph, name):
+        return lambda: _abi.check(lib.tnpa_backward_phase(ctypes.byref(prob), ctypes.byref(grads), ph, st), name)
     fwd = lambda: _abi.check(lib.tnpa_forward(ctypes.byref(prob), ctypes.byref(od), st), "fwd")  # noqa: E731
-    kv = lambda: _abi.check(lib.tnpa_backward_phase(ctypes.byref(prob), ctypes.byref(grads), _abi.PHASE_KV, st), "kv")  # noqa: E731,E501
-    qq = lambda: _abi.check(lib.tnpa_backward_phase(ctypes.byref(prob), ctypes.byref(grads), _abi.PHASE_Q, st), "q")  # noqa: E731,E501
     out = {}
-    for name, fn in (("fwd", fwd), ("bwd_kv", kv), ("bwd_q", qq)):
+    for name, fn in (("fwd", fwd), ("bwd_scale", phase(_abi.PHASE_KV_SCALE, "scale")),
+                     ("bwd_dv", phase(_abi.PHASE_KV_DV, "dv")), ("bwd_dk", phase(_abi.PHASE_KV_DK, "dk")),
+                     ("bwd_q", phase(_abi.PHASE_Q, "q"))):
         for _ in range(3):
             fn()
         torch.cuda.synchronize()
@@ -188,8 +190,10 @@ def main(argv=None):
     value = fl_step / (ms * 1e-3) / 1e12
 
     kt = kernel_times(q.detach(), k.detach(), v.detach(), do, doc, rs, degree, a.kernel_reps)
-    units = {"fwd": 2, "bwd_kv": 4, "bwd_q": 3}  # matmul units of 2*B*H*Npairs*D each kernel performs
-    dom = max(kt, key=kt.get)
+    # matmul units of 2*B*H*Npairs*D each kernel executes: fwd QK^T + PV; dV pass S + dV; dK pass S + dP + dK;
+    # dQ pass S + dP + dQ (the row-scaling pass is a bandwidth kernel with no matrix work)
+    units = {"fwd": 2, "bwd_dv": 2, "bwd_dk": 3, "bwd_q": 3}
+    dom = max(units, key=lambda n: kt[n])
     ach = units[dom] * 2.0 * B * H * npairs(T) * D / (kt[dom] * 1e-3) / 1e12
     line = {
         "metric": METRIC, "value": round(value, 2), "unit": "TFLOP/s", "n_gpus": 1, "steps": a.steps,

@@ -103,12 +103,20 @@ int64_t tnpa_dpar_workspace_floats(const tnpa_problem_t* problem);
  * every reduction in a fixed order. */
 int tnpa_backward(const tnpa_problem_t* problem, const tnpa_grads_t* grads, void* stream);
 
-/* The two passes of tnpa_backward, selectable: TNPA_PHASE_KV writes dk1, (dk2), dv and dpar (ref _bwd_kv,
+/* The passes of tnpa_backward, selectable: TNPA_PHASE_KV writes dk1, (dk2), dv and dpar (ref _bwd_kv,
  * tnlm/kernels/poly_attn.py:298-299,304-306); TNPA_PHASE_Q writes dq1, (dq2) (ref _bwd_q, :302-303). The passes
  * read only inputs, so they may run on different streams concurrently. Gradients a phase does not write may be
- * left NULL. tnpa_backward(...) == tnpa_backward_phase(..., TNPA_PHASE_KV | TNPA_PHASE_Q, ...). */
+ * left NULL. tnpa_backward(...) == tnpa_backward_phase(..., TNPA_PHASE_KV | TNPA_PHASE_Q, ...).
+ * For 16-bit inputs with one q/k pair the key side is itself three launches, selectable instead of TNPA_PHASE_KV:
+ * TNPA_PHASE_KV_SCALE writes dout_scaled (required), TNPA_PHASE_KV_DV writes dv, TNPA_PHASE_KV_DK writes dk1 and
+ * dpar; the dV and dK passes read dout_scaled as already written when its data is not NULL, and scale dout
+ * themselves otherwise. Other configurations run dK and dV in one kernel and accept only the two together
+ * (TNPA_ERR_UNSUPPORTED otherwise). */
 #define TNPA_PHASE_KV 1
 #define TNPA_PHASE_Q 2
+#define TNPA_PHASE_KV_SCALE 4
+#define TNPA_PHASE_KV_DV 8
+#define TNPA_PHASE_KV_DK 16
 int tnpa_backward_phase(const tnpa_problem_t* problem, const tnpa_grads_t* grads, int32_t phases, void* stream);
 
 #ifdef __cplusplus

@@ -51,7 +51,7 @@ _SIGNATURES = {
     "tnpa_backward_phase": (ctypes.c_int, [ctypes.POINTER(Problem), ctypes.POINTER(Grads), ctypes.c_int32,
                                            ctypes.c_void_p]),
 }
-PHASE_KV, PHASE_Q = 1, 2
+PHASE_KV, PHASE_Q, PHASE_KV_SCALE, PHASE_KV_DV, PHASE_KV_DK = 1, 2, 4, 8, 16
 
 _LIB = None
 

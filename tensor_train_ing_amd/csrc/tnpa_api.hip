@@ -298,20 +298,35 @@ int tnpa_backward_phase(const tnpa_problem_t* problem, const tnpa_grads_t* grads
   int rc = check_problem(problem);
   if (rc) return rc;
   if (grads == nullptr) return fail(TNPA_ERR_INVALID, "null grads");
-  if (phases <= 0 || phases > (TNPA_PHASE_KV | TNPA_PHASE_Q))
-    return fail(TNPA_ERR_INVALID, "phases must be a nonzero combination of TNPA_PHASE_KV and TNPA_PHASE_Q");
+  constexpr int ALL = TNPA_PHASE_KV | TNPA_PHASE_Q | TNPA_PHASE_KV_SCALE | TNPA_PHASE_KV_DV | TNPA_PHASE_KV_DK;
+  constexpr int KV_PARTS = TNPA_PHASE_KV_SCALE | TNPA_PHASE_KV_DV | TNPA_PHASE_KV_DK;
+  if (phases <= 0 || (phases & ~ALL) != 0)
+    return fail(TNPA_ERR_INVALID, "phases must be a nonzero combination of the TNPA_PHASE_* flags");
+  if ((phases & TNPA_PHASE_KV) && (phases & KV_PARTS))
+    return fail(TNPA_ERR_INVALID, "TNPA_PHASE_KV already includes the TNPA_PHASE_KV_* parts");
   const tnpa_problem_t& p = *problem;
   const int es = esize(p.dtype);
-  const bool kv = phases & TNPA_PHASE_KV, q = phases & TNPA_PHASE_Q;
+  const bool split = tnpa::kv_split(p.dtype == TNPA_F32, poly_of(p));
+  const int kvsel = (phases & TNPA_PHASE_KV) ? 3 : ((phases & TNPA_PHASE_KV_DV) ? 1 : 0) | ((phases & TNPA_PHASE_KV_DK) ? 2 : 0);
+  if (!split && (kvsel == 1 || kvsel == 2))
+    return fail(TNPA_ERR_UNSUPPORTED, "this configuration computes dK and dV in one kernel: ask for both passes");
+  const bool scale_only = (phases & TNPA_PHASE_KV_SCALE) != 0;
+  if (scale_only && grads->dout_scaled.data == nullptr)
+    return fail(TNPA_ERR_INVALID, "TNPA_PHASE_KV_SCALE needs dout_scaled");
+  const bool kv = kvsel != 0, q = phases & TNPA_PHASE_Q;
+  const bool want_dv = kvsel & 1, want_dk = kvsel & 2;
   if ((rc = check_tensor(grads->dout, "dout", p, es))) return rc;
   if (q && (rc = check_tensor(grads->dq1, "dq1", p, es))) return rc;
-  if (kv && (rc = check_tensor(grads->dk1, "dk1", p, es))) return rc;
-  if (kv && (rc = check_tensor(grads->dv, "dv", p, es))) return rc;
+  if (want_dk && (rc = check_tensor(grads->dk1, "dk1", p, es))) return rc;
+  if (want_dv && (rc = check_tensor(grads->dv, "dv", p, es))) return rc;
   if (two_pairs(p.kind)) {
     if (q && (rc = check_tensor(grads->dq2, "dq2", p, es))) return rc;
-    if (kv && (rc = check_tensor(grads->dk2, "dk2", p, es))) return rc;
+    if (want_dk && (rc = check_tensor(grads->dk2, "dk2", p, es))) return rc;
   }
-  const bool par = kv && (p.kind == TNPA_OFFSET_SQUARE || p.kind == TNPA_LOWER_DEGREE_MIX);
+  if (grads->dout_scaled.data != nullptr && (kv || scale_only) &&
+      (rc = check_tensor(grads->dout_scaled, "dout_scaled", p, es)))
+    return rc;
+  const bool par = want_dk && (p.kind == TNPA_OFFSET_SQUARE || p.kind == TNPA_LOWER_DEGREE_MIX);
   if (par && (grads->dpar_partial == nullptr || grads->dpar == nullptr))
     return fail(TNPA_ERR_INVALID, "offset_square / lower_degree_mix need dpar_partial and dpar");
   tnpa::KParams k = make_params(p);
@@ -320,24 +335,27 @@ int tnpa_backward_phase(const tnpa_problem_t* problem, const tnpa_grads_t* grads
     k.dq1 = desc(grads->dq1);
     k.dq2 = two_pairs(p.kind) ? desc(grads->dq2) : desc(grads->dq1);
   }
-  if (kv) {
+  if (want_dk) {
     k.dk1 = desc(grads->dk1);
     k.dk2 = two_pairs(p.kind) ? desc(grads->dk2) : desc(grads->dk1);
-    k.dv = desc(grads->dv);
   }
+  if (want_dv) k.dv = desc(grads->dv);
+  k.kvsel = kvsel;
   k.dpar = par ? grads->dpar_partial : nullptr;
   hipError_t e;
-  const bool pre = kv && grads->dout_scaled.data != nullptr;
-  if (pre) {
-    if ((rc = check_tensor(grads->dout_scaled, "dout_scaled", p, es))) return rc;
+  // the full key-side phase writes the scaled dO itself; the separate passes read what TNPA_PHASE_KV_SCALE wrote
+  const bool write_scaled = grads->dout_scaled.data != nullptr && ((phases & TNPA_PHASE_KV) || scale_only);
+  if (grads->dout_scaled.data != nullptr && kv) {
+    k.dsc = desc(grads->dout_scaled);
+    k.dpre = 1;
+  }
+  if (write_scaled) {
     switch (p.dtype) {
       case TNPA_BF16: e = scale_rows<__bf16>(p, grads->dout, grads->dout_scaled, (hipStream_t)stream); break;
       case TNPA_F16: e = scale_rows<_Float16>(p, grads->dout, grads->dout_scaled, (hipStream_t)stream); break;
       default: e = scale_rows<float>(p, grads->dout, grads->dout_scaled, (hipStream_t)stream); break;
     }
     if (e != hipSuccess) return fail(TNPA_ERR_LAUNCH, "tnpa_backward (row scaling): %s", hipGetErrorString(e));
-    k.dsc = desc(grads->dout_scaled);
-    k.dpre = 1;
   }
   if (kv) {
     e = run(PH_BWD_KV, p, k, (hipStream_t)stream);

@@ -860,10 +860,12 @@ template <typename T, int POLY, int DK, int DV> hipError_t launch_bwd_kv(const K
   static_assert(C::KV_KEYS == KV_BLOCK_KEYS, "dK/dV block size is fixed");
   const int grid = p.B * p.H * ((p.T + C::KV_KEYS - 1) / C::KV_KEYS);
   if constexpr (C::KV_SPLIT) {
-    hipLaunchKernelGGL((k_bwd_kv<T, POLY, DK, DV, C::KV_NW, C::KV_KW, C::KV_BM, 2, KV_DV>), dim3(grid), dim3(C::KV_NW * 64),
-                       0, st, p);
-    hipLaunchKernelGGL((k_bwd_kv<T, POLY, DK, DV, C::KV_NW, C::KV_KW, C::KV_BM, 2, KV_DK>), dim3(grid), dim3(C::KV_NW * 64),
-                       0, st, p);
+    if (p.kvsel & 1)
+      hipLaunchKernelGGL((k_bwd_kv<T, POLY, DK, DV, C::KV_NW, C::KV_KW, C::KV_BM, 2, KV_DV>), dim3(grid),
+                         dim3(C::KV_NW * 64), 0, st, p);
+    if (p.kvsel & 2)
+      hipLaunchKernelGGL((k_bwd_kv<T, POLY, DK, DV, C::KV_NW, C::KV_KW, C::KV_BM, 2, KV_DK>), dim3(grid),
+                         dim3(C::KV_NW * 64), 0, st, p);
   } else {
     hipLaunchKernelGGL((k_bwd_kv<T, POLY, DK, DV, C::KV_NW, C::KV_KW, C::KV_BM, C::KV_WPE, KV_BOTH>), dim3(grid),
                        dim3(C::KV_NW * 64), 0, st, p);

@@ -28,6 +28,7 @@ struct KParams {
   const float* offs;   // (H) offset_square offsets or null
   float* dpar;         // (B*H, NNB, 4) per-key-block partial sums for dcoef / db, or null
   int dpre;            // 1: dsc holds the row-scaled dout; 0: the dK/dV pass scales dout while staging it
+  int kvsel;           // key-side kernels to launch: 1 = dV pass, 2 = dK pass, 3 = both (or the combined kernel)
   int B, H, T;
   int kind, deg;
   float sm;  // 1/sqrt(dk)
@@ -36,6 +37,9 @@ struct KParams {
 };
 
 constexpr int KV_BLOCK_KEYS = 128;  // keys per dK/dV workgroup for every configuration (sizes the dpar workspace)
+
+// Whether the key side runs as separate dV and dK passes (16-bit inputs, one q/k pair); mirrors Cfg::KV_SPLIT.
+inline bool kv_split(bool f32, int poly) { return !f32 && poly != POLY_GEN2; }
 
 template <typename T, int POLY, int DK, int DV> hipError_t launch_fwd(const KParams& p, hipStream_t st);
 template <typename T, int POLY, int DK, int DV> hipError_t launch_bwd_kv(const KParams& p, hipStream_t st);

@@ -121,7 +121,18 @@ def test_misaligned_views_and_missing_parameters_are_rejected(lib):
     assert lib.tnpa_backward(ctypes.byref(p), ctypes.byref(g), None) == _abi.ERR_INVALID
     assert "dpar" in lib.tnpa_last_error().decode()
     assert lib.tnpa_backward_phase(ctypes.byref(_problem()), ctypes.byref(g), 0, None) == _abi.ERR_INVALID
-    assert lib.tnpa_backward_phase(ctypes.byref(_problem()), ctypes.byref(g), 4, None) == _abi.ERR_INVALID
+    assert lib.tnpa_backward_phase(ctypes.byref(_problem()), ctypes.byref(g), 32, None) == _abi.ERR_INVALID
+    # the key-side parts: not together with the whole key side, the scaling part needs its workspace, and only the
+    # split configurations (16-bit, one q/k pair) run dV or dK alone
+    both = _abi.PHASE_KV | _abi.PHASE_KV_DV
+    assert lib.tnpa_backward_phase(ctypes.byref(_problem()), ctypes.byref(g), both, None) == _abi.ERR_INVALID
+    assert lib.tnpa_backward_phase(ctypes.byref(_problem()), ctypes.byref(g), _abi.PHASE_KV_SCALE,
+                                   None) == _abi.ERR_INVALID
+    assert "dout_scaled" in lib.tnpa_last_error().decode()
+    f32 = _problem(dtype=_abi.F32)
+    assert lib.tnpa_backward_phase(ctypes.byref(f32), ctypes.byref(g), _abi.PHASE_KV_DV, None) == _abi.ERR_UNSUPPORTED
+    two = _problem(kind=_abi.SIGNED_PRODUCT)
+    assert lib.tnpa_backward_phase(ctypes.byref(two), ctypes.byref(g), _abi.PHASE_KV_DK, None) == _abi.ERR_UNSUPPORTED
     assert lib.tnpa_doc_bounds(None, 1, 128, 2, 128, None, None, None) == _abi.ERR_INVALID
     assert lib.tnpa_doc_bounds(ctypes.c_void_p(4096), 1, 64, 2, 128, ctypes.c_void_p(4096), ctypes.c_void_p(4096),
                                None) == _abi.ERR_INVALID

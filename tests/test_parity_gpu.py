@@ -277,9 +277,10 @@ def test_prescaled_dout_matches_in_pass_scaling(kind, dtype):
     coef, bb = _params(H)
     dstart, qend = doc_bounds(docs)
     K = KINDS[kind]
-    prob = _problem(K, 2, q1, k1, q2 if two else q1, k2 if two else k1, v, dstart, qend, rs.float().contiguous(),
-                    coef.float().contiguous() if kind == "lower_degree_mix" else None,
-                    bb.float().contiguous() if kind == "offset_square" else None)
+    # every tensor whose pointer goes into the problem struct stays referenced for the whole test
+    rs_f, coef_f, b_f = rs.float().contiguous(), coef.float().contiguous(), bb.float().contiguous()
+    prob = _problem(K, 2, q1, k1, q2 if two else q1, k2 if two else k1, v, dstart, qend, rs_f,
+                    coef_f if kind == "lower_degree_mix" else None, b_f if kind == "offset_square" else None)
     lib = _abi.load()
     outs = []
     for pre in (False, True):
@@ -296,6 +297,41 @@ def test_prescaled_dout_matches_in_pass_scaling(kind, dtype):
     for a, b2 in zip(*outs):
         if a is not None:
             assert torch.equal(a, b2)
+
+
+@pytest.mark.parametrize("kind", ["power", "offset_square"])
+def test_key_side_parts_equal_the_whole_pass(kind):
+    """TNPA_PHASE_KV_SCALE, then TNPA_PHASE_KV_DV and TNPA_PHASE_KV_DK as separate calls, give bit-identical dK, dV
+    and dpar to one TNPA_PHASE_KV call."""
+    import ctypes
+    from tensor_train_ing_amd import _abi
+    from tensor_train_ing_amd.poly_attn import KINDS, _desc, _problem, _stream, doc_bounds
+    B, H, T, D = 2, 2, 260, 128
+    q1, k1, _, _, v, dout = (None if x is None else x.cuda()
+                             for x in gaussian_inputs(B, H, T, D, D, torch.bfloat16, 12, qk_scale=D ** -0.25))
+    docs = _doc_rows(B, T).cuda()
+    dstart, qend = doc_bounds(docs)
+    coef, bb = _params(H)
+    # every tensor whose pointer goes into the problem struct stays referenced for the whole test
+    rs = row_scale(docs, 1.0).float().contiguous()
+    b_f = bb.float().contiguous()
+    prob = _problem(KINDS[kind], 2, q1, k1, q1, k1, v, dstart, qend, rs, None,
+                    b_f if kind == "offset_square" else None)
+    lib = _abi.load()
+    st = _stream(q1.device)
+    res = []
+    for parts in ((_abi.PHASE_KV,), (_abi.PHASE_KV_SCALE, _abi.PHASE_KV_DV, _abi.PHASE_KV_DK)):
+        dk1, dv, dos = torch.empty_like(k1), torch.empty_like(v), torch.empty_like(dout)
+        ws = torch.empty(max(1, lib.tnpa_dpar_workspace_floats(ctypes.byref(prob))), device="cuda")
+        dpar = torch.zeros(H, 4, device="cuda")
+        g = _abi.Grads(_desc(dout), _abi.Tensor(), _desc(dk1), _abi.Tensor(), _desc(dk1), _desc(dv),
+                       ws.data_ptr(), dpar.data_ptr(), _desc(dos))
+        for ph in parts:
+            _abi.check(lib.tnpa_backward_phase(ctypes.byref(prob), ctypes.byref(g), ph, st), "kv part")
+        torch.cuda.synchronize()
+        res.append((dk1, dv, dpar))
+    for a, b2 in zip(*res):
+        assert torch.equal(a, b2)
 
 
 # ------------------------------------------------------------------ BASELINE.json configurations, full size
