@@ -36,10 +36,12 @@ struct KParams {
   float gf;  // factor on dQ and dK (p*sm^p, sm^2 or sm)
 };
 
-constexpr int KV_BLOCK_KEYS = 128;  // keys per dK/dV workgroup for every configuration (sizes the dpar workspace)
-
 // Whether the key side runs as separate dV and dK passes (16-bit inputs, one q/k pair); mirrors Cfg::KV_SPLIT.
 inline bool kv_split(bool f32, int poly) { return !f32 && poly != POLY_GEN2; }
+
+// Keys per dK/dV workgroup (sizes the dcoef/db partials); mirrors Cfg::KV_KEYS: eight waves of 32 keys for the split
+// passes (two waves per SIMD), four for the one-wave-per-SIMD combined kernel.
+inline int kv_block_keys(bool f32, int poly) { return kv_split(f32, poly) ? 256 : 128; }
 
 template <typename T, int POLY, int DK, int DV> hipError_t launch_fwd(const KParams& p, hipStream_t st);
 template <typename T, int POLY, int DK, int DV> hipError_t launch_bwd_kv(const KParams& p, hipStream_t st);

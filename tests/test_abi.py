@@ -143,6 +143,8 @@ def test_dpar_workspace_size(lib):
     assert lib.tnpa_dpar_workspace_floats(ctypes.byref(_problem())) == 0
     p = _problem(kind=_abi.LOWER_DEGREE_MIX, seq_len=300)
     assert lib.tnpa_dpar_workspace_floats(ctypes.byref(p)) == 2 * 2 * 3 * 4  # ceil(300 / 128) key blocks
+    p = _problem(kind=_abi.OFFSET_SQUARE, seq_len=300)  # bf16, one pair: split passes with 256-key blocks
+    assert lib.tnpa_dpar_workspace_floats(ctypes.byref(p)) == 2 * 2 * 2 * 4
 
 
 def test_python_operator_errors_mirror_the_reference():
