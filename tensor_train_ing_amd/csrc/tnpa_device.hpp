@@ -220,6 +220,36 @@ template <typename T, int ROWS, int D, int WID, int NT> struct Stage {
       }
     }
   }
+  // Chunk i through a buffer resource over the tile's rows (rows past the resource's end read as zero): one
+  // instruction, no address arithmetic or branch, so it can sit between matrix instructions. voff = byte offset of
+  // the thread's chunk i inside the tile. Needs TOTAL % NT == 0.
+  __device__ inline void load_buf(int i, __amdgpu_buffer_rsrc_t rs, uint32_t voff) {
+    r[i] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rs, (int)voff, 0, 0));
+  }
+  // byte offset of the thread's chunk i inside a tile of row stride st (elements)
+  __device__ static inline uint32_t chunk_off(int i, int64_t st) {
+    const int idx = (int)threadIdx.x + i * NT;
+    return (uint32_t)(((int64_t)(idx / NCHG) * st + (idx % NCHG) * CE) * (int64_t)sizeof(T));
+  }
+  __device__ inline void store_raw(int i, char TNPA_LDS* tile) const {
+    const int idx = (int)threadIdx.x + i * NT;
+    *(u32x4 TNPA_LDS*)(tile + TL::off(idx / NCHG, (idx % NCHG) * CE)) = r[i];
+  }
+  // Branch-free form of load() for one chunk, so it can be scheduled between matrix instructions: the row is clamped
+  // to rmax (a valid row) instead of skipped; store_chunk() zeroes rows at or beyond nvalid. Needs TOTAL % NT == 0.
+  __device__ inline void load_chunk(int i, const T* __restrict__ g, int64_t st, int row0, int rmax) {
+    static_assert(TOTAL % NT == 0, "every thread owns PER chunks");
+    const int idx = (int)threadIdx.x + i * NT;
+    const int rr = idx / NCHG, c = idx % NCHG;
+    r[i] = *(const u32x4*)(g + (int64_t)min(row0 + rr, rmax) * st + c * CE);
+  }
+  __device__ inline void store_chunk(int i, char TNPA_LDS* tile, int nvalid) const {
+    const int idx = (int)threadIdx.x + i * NT;
+    const int rr = idx / NCHG, c = idx % NCHG;
+    const bool ok = rr < nvalid;
+    *(u32x4 TNPA_LDS*)(tile + TL::off(rr, c * CE)) =
+        u32x4{ok ? r[i][0] : 0u, ok ? r[i][1] : 0u, ok ? r[i][2] : 0u, ok ? r[i][3] : 0u};
+  }
 };
 
 // Stores 4 consecutive output elements (one accumulator register group) converted to T.

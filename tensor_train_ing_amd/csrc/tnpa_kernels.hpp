@@ -137,7 +137,10 @@ k_fwd(const KParams p) {
   typedef Tile<T, BN, DKP> KTile;
   typedef Tile<T, BN, DVP> VTile;
   constexpr int BUF = NPAIR * KTile::BYTES + VTile::BYTES;
-  __shared__ __attribute__((aligned(16))) char smem_[2 * BUF];
+  // three tile buffers for the pipelined unmasked run when they fit the 160 KB of LDS, else two
+  constexpr bool CHUNKED = Stage<T, BN, DK, DKP, NT>::TOTAL % NT == 0 && Stage<T, BN, DV, DVP, NT>::TOTAL % NT == 0;
+  constexpr int NBUF = CHUNKED && NKB >= 2 && 3 * BUF <= 160 * 1024 ? 3 : 2;
+  __shared__ __attribute__((aligned(16))) char smem_[NBUF * BUF];
   char TNPA_LDS* smem = (char TNPA_LDS*)smem_;
 
   const int T_ = p.T, BH = p.B * p.H;
@@ -156,7 +159,7 @@ k_fwd(const KParams p) {
   const float* rsc = p.rscale + (int64_t)b * T_;
 
   if constexpr (DKP != DK || DVP != DV) {
-    for (int i = threadIdx.x; i < 2 * BUF / 16; i += NT) ((u32x4 TNPA_LDS*)smem)[i] = u32x4{0u, 0u, 0u, 0u};
+    for (int i = threadIdx.x; i < NBUF * BUF / 16; i += NT) ((u32x4 TNPA_LDS*)smem)[i] = u32x4{0u, 0u, 0u, 0u};
     __syncthreads();
   }
 
@@ -248,44 +251,220 @@ k_fwd(const KParams p) {
       }
   };
 
-  // One tile step: prefetch the next K/V tile into registers, compute on the current LDS buffer, publish the
-  // prefetched tile into the other buffer, one barrier.
-  auto step = [&](const int n0, auto fast_c) {
-    constexpr bool FAST = decltype(fast_c)::value;
-    const bool more = n0 + BN < hi;
-    if (more) {
+  typedef Stage<T, BN, DK, DKP, NT> KStage;
+  typedef Stage<T, BN, DV, DVP, NT> VStage;
+  auto next_buf = [](const int c) { return c + 1 == NBUF ? 0 : c + 1; };
+  // Global -> register staging of the tile at rows n1.. and its store into an LDS buffer. The chunked form is
+  // branch-free (clamped rows, zeroed in the store), so it can sit between matrix instructions.
+  auto stage_load = [&](const int n1) {
+    if constexpr (CHUNKED) {
 #pragma unroll
-      for (int pr = 0; pr < NPAIR; ++pr) sk[pr].load(kp[pr], kst[pr], n0 + BN, T_ - n0 - BN);
-      sv.load(vp, p.v.st, n0 + BN, T_ - n0 - BN);
-    }
-    const char TNPA_LDS* base = smem + cur * BUF;
-    if constexpr (FAST) {
+      for (int pr = 0; pr < NPAIR; ++pr)
 #pragma unroll
-      for (int kb = 0; kb < NKB; ++kb) sub(base, n0, kb, 0u, 0u, std::true_type{}, std::true_type{});
+        for (int i = 0; i < KStage::PER; ++i) sk[pr].load_chunk(i, kp[pr], kst[pr], n1, T_ - 1);
+#pragma unroll
+      for (int i = 0; i < VStage::PER; ++i) sv.load_chunk(i, vp, p.v.st, n1, T_ - 1);
     } else {
 #pragma unroll
-      for (int kb = 0; kb < NKB; ++kb) {
-        const int key0 = n0 + 32 * kb;
-        uint32_t am = 0, fm = 0;
+      for (int pr = 0; pr < NPAIR; ++pr) sk[pr].load(kp[pr], kst[pr], n1, T_ - n1);
+      sv.load(vp, p.v.st, n1, T_ - n1);
+    }
+  };
+  auto stage_store = [&](char TNPA_LDS* dstb, const int n1) {
+    if constexpr (CHUNKED) {
 #pragma unroll
-        for (int s = 0; s < QW; ++s) {
-          if (qa[s] < T_ && key0 <= ql[s] && key0 + 31 >= dsa[s]) am |= 1u << s;
-          if (key0 + 31 <= qa[s] && dsl[s] <= key0) fm |= 1u << s;
+      for (int pr = 0; pr < NPAIR; ++pr)
+#pragma unroll
+        for (int i = 0; i < KStage::PER; ++i) sk[pr].store_chunk(i, dstb + pr * KTile::BYTES, T_ - n1);
+#pragma unroll
+      for (int i = 0; i < VStage::PER; ++i) sv.store_chunk(i, dstb + NPAIR * KTile::BYTES, T_ - n1);
+    } else {
+#pragma unroll
+      for (int pr = 0; pr < NPAIR; ++pr) sk[pr].store(dstb + pr * KTile::BYTES);
+      sv.store(dstb + NPAIR * KTile::BYTES);
+    }
+  };
+  auto k_rows = [&](Op (&ka)[NPAIR][NCK], const char TNPA_LDS* base, const int kb) {
+#pragma unroll
+    for (int pr = 0; pr < NPAIR; ++pr)
+#pragma unroll
+      for (int c = 0; c < NCK; ++c) ka[pr][c] = read_row<T, KTile>(base + pr * KTile::BYTES, 32 * kb, kappa<T>(l32), c, h);
+  };
+  auto v_cols = [&](Op (&vt)[NDV][NC2], const char TNPA_LDS* base, const int kb) {
+#pragma unroll
+    for (int d = 0; d < NDV; ++d)
+#pragma unroll
+      for (int c2 = 0; c2 < NC2; ++c2)
+        vt[d][c2] = read_col<T, VTile>(base + NPAIR * KTile::BYTES, 32 * kb + c2 * KC, 32 * d, lane);
+  };
+  auto s_mma = [&](f32x16 (&sacc)[NPAIR][QW], const Op (&ka)[NPAIR][NCK]) {
+#pragma unroll
+    for (int pr = 0; pr < NPAIR; ++pr)
+#pragma unroll
+      for (int s = 0; s < QW; ++s) sacc[pr][s] = zero16();
+#pragma unroll
+    for (int c = 0; c < NCK; ++c)
+#pragma unroll
+      for (int pr = 0; pr < NPAIR; ++pr)
+#pragma unroll
+        for (int s = 0; s < QW; ++s) sacc[pr][s] = M::mma(ka[pr][c], qf[pr][s][c], sacc[pr][s]);
+  };
+  auto power = [&](Op (&pop)[QW][NC2], const f32x16 (&sacc)[NPAIR][QW]) {
+#pragma unroll
+    for (int s = 0; s < QW; ++s) {
+      float pv[16];
+#pragma unroll
+      for (int r = 0; r < 16; ++r) pv[r] = poly_value<POLY>(sacc[0][s][r], sacc[NPAIR - 1][s][r], p.kind, p.deg, p.sm, cf);
+#pragma unroll
+      for (int c2 = 0; c2 < NC2; ++c2) pop[s][c2] = M::cvt(pv + c2 * EPL);
+    }
+  };
+  // c2-major: consecutive MFMAs go to different accumulators
+  auto pv_mma = [&](const Op (&vt)[NDV][NC2], const Op (&pop)[QW][NC2]) {
+#pragma unroll
+    for (int c2 = 0; c2 < NC2; ++c2)
+#pragma unroll
+      for (int d = 0; d < NDV; ++d)
+#pragma unroll
+        for (int s = 0; s < QW; ++s) oacc[s][d] = M::mma(vt[d][c2], pop[s][c2], oacc[s][d]);
+  };
+  // Buffer resource over rows n1.. of one head: rows at or past T_ read as zero.
+  auto rows_rsrc = [&](const T* base, const int64_t st, const int n1, const int D) {
+    const int64_t rem = n1 < T_ ? ((int64_t)(T_ - 1 - n1) * st + D) * (int64_t)sizeof(T) : 0;
+    const int nrec = (int)(rem < 0x7fffffff ? rem : 0x7fffffff);
+    return __builtin_amdgcn_make_buffer_rsrc((void*)(base + (int64_t)n1 * st), (short)0, nrec, 0x00020000);
+  };
+  uint32_t kvo[NPAIR][KStage::PER], vvo[VStage::PER];
+#pragma unroll
+  for (int pr = 0; pr < NPAIR; ++pr)
+#pragma unroll
+    for (int i = 0; i < KStage::PER; ++i) kvo[pr][i] = KStage::chunk_off(i, kst[pr]);
+#pragma unroll
+  for (int i = 0; i < VStage::PER; ++i) vvo[i] = VStage::chunk_off(i, p.v.st);
+  auto stage_load_buf = [&](const int n1) {
+    if constexpr (!CHUNKED) return;
+#pragma unroll
+    for (int pr = 0; pr < NPAIR; ++pr) {
+      const auto rs = rows_rsrc(kp[pr], kst[pr], n1, DK);
+#pragma unroll
+      for (int i = 0; i < KStage::PER; ++i) sk[pr].load_buf(i, rs, kvo[pr][i]);
+    }
+    const auto rs = rows_rsrc(vp, p.v.st, n1, DV);
+#pragma unroll
+    for (int i = 0; i < VStage::PER; ++i) sv.load_buf(i, rs, vvo[i]);
+  };
+  auto stage_store_raw = [&](char TNPA_LDS* dstb) {
+#pragma unroll
+    for (int pr = 0; pr < NPAIR; ++pr)
+#pragma unroll
+      for (int i = 0; i < KStage::PER; ++i) sk[pr].store_raw(i, dstb + pr * KTile::BYTES);
+#pragma unroll
+    for (int i = 0; i < VStage::PER; ++i) sv.store_raw(i, dstb + NPAIR * KTile::BYTES);
+  };
+
+  // Run of unmasked tiles jb..je-1 (no mask, no sub-block test).
+  // Three buffers: software pipeline over the run's 32-key sub-blocks g. Phase A(g): the V^T(g) reads and the
+  // S(g+1) MFMA chain, back to back; phase B(g): O += V^T(g) P(g) MFMAs, with the power of S(g+1) and the K-row
+  // reads of g+2 between them. Every operand is read a phase ahead and the VALU work sits between independent
+  // MFMAs, so one wave keeps the matrix pipe fed on its own. Tile j+1 is published by the barrier at the start of
+  // B(NKB-2) of tile j, before the first read of its rows; its buffer loads are issued after the previous barrier
+  // and written to LDS in A(NKB-2) (tiles j, j+1 and j+2 in flight). Two buffers: one tile per step, loads
+  // before and stores after the compute.
+  auto fast_run = [&](const int jb, const int je) {
+    if constexpr (NBUF == 3) {
+      Op ka[NPAIR][NCK], vt[NDV][NC2], pop[QW][NC2], pn[QW][NC2];
+      f32x16 sn[NPAIR][QW];
+      stage_load_buf(lo + (jb + 1) * BN);  // the step before the run staged only tile jb
+      k_rows(ka, smem + cur * BUF, 0);
+      s_mma(sn, ka);
+      k_rows(ka, smem + cur * BUF, 1);
+      power(pop, sn);
+      // one tile; LAST (the run's final tile) drains the pipeline instead of starting the next tile
+      auto tile = [&](const int j, auto last_c) {
+        constexpr bool LAST = decltype(last_c)::value;
+        const int nc = next_buf(cur);
+        const char TNPA_LDS* base = smem + cur * BUF;
+        char TNPA_LDS* b1 = smem + nc * BUF;
+        const int n1 = lo + (j + 1) * BN;
+#pragma unroll
+        for (int kb = 0; kb < NKB; ++kb) {
+          const bool more_s = kb + 1 < NKB || !LAST;
+          v_cols(vt, base, kb);
+          if (kb == NKB - 2) stage_store_raw(b1);
+          if (more_s) s_mma(sn, ka);
+          __builtin_amdgcn_sched_barrier(0);
+          if (kb == NKB - 2) {
+            __syncthreads();
+            if (!LAST) stage_load_buf(n1 + BN);
+          }
+          if (kb + 2 < NKB) k_rows(ka, base, kb + 2);
+          else if (!LAST) k_rows(ka, b1, kb + 2 - NKB);
+          pv_mma(vt, pop);
+          if (more_s) power(pn, sn);
+          // K-row reads first (a whole phase ahead of their use), then one MFMA per few VALU of the power
+          if (kb + 2 < NKB || !LAST) __builtin_amdgcn_sched_group_barrier(0x100, NPAIR * NCK, 0);
+#pragma unroll
+          for (int i = 0; i < NDV * NC2 * QW; ++i) {
+            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+            __builtin_amdgcn_sched_group_barrier(0x002, 4, 0);
+          }
+          __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+          for (int s = 0; s < QW; ++s)
+#pragma unroll
+            for (int c2 = 0; c2 < NC2; ++c2) pop[s][c2] = pn[s][c2];
         }
-        am = __builtin_amdgcn_readfirstlane(am);
-        fm = __builtin_amdgcn_readfirstlane(fm);
-        if (am == 0) continue;
-        sub(base, n0, kb, am, fm, std::false_type{}, std::false_type{});
+        cur = nc;
+      };
+      for (int j = jb; j + 1 < je; ++j) tile(j, std::false_type{});
+      tile(je - 1, std::true_type{});
+    } else {
+      for (int j = jb; j < je; ++j) {
+        const int n1 = lo + (j + 1) * BN;
+        const bool more = n1 < hi;
+        const char TNPA_LDS* base = smem + cur * BUF;
+        if (more) stage_load(n1);
+#pragma unroll
+        for (int kb = 0; kb < NKB; ++kb) {
+          Op ka[NPAIR][NCK], vt[NDV][NC2], pop[QW][NC2];
+          f32x16 sacc[NPAIR][QW];
+          k_rows(ka, base, kb);
+          v_cols(vt, base, kb);
+          s_mma(sacc, ka);
+          power(pop, sacc);
+          pv_mma(vt, pop);
+        }
+        if (more) stage_store(smem + next_buf(cur) * BUF, n1);
+        __syncthreads();
+        cur = next_buf(cur);
       }
     }
-    if (more) {
-      char TNPA_LDS* nxt = smem + (cur ^ 1) * BUF;
+  };
+
+  // One masked tile step: prefetch the next K/V tile into registers, compute on the current LDS buffer, publish
+  // the prefetched tile into the next buffer, one barrier.
+  auto step = [&](const int n0) {
+    const int n1 = n0 + BN;
+    const bool more = n1 < hi;
+    if (more) stage_load(n1);
+    const char TNPA_LDS* base = smem + cur * BUF;
 #pragma unroll
-      for (int pr = 0; pr < NPAIR; ++pr) sk[pr].store(nxt + pr * KTile::BYTES);
-      sv.store(nxt + NPAIR * KTile::BYTES);
+    for (int kb = 0; kb < NKB; ++kb) {
+      const int key0 = n0 + 32 * kb;
+      uint32_t am = 0, fm = 0;
+#pragma unroll
+      for (int s = 0; s < QW; ++s) {
+        if (qa[s] < T_ && key0 <= ql[s] && key0 + 31 >= dsa[s]) am |= 1u << s;
+        if (key0 + 31 <= qa[s] && dsl[s] <= key0) fm |= 1u << s;
+      }
+      am = __builtin_amdgcn_readfirstlane(am);
+      fm = __builtin_amdgcn_readfirstlane(fm);
+      if (am == 0) continue;
+      sub(base, n0, kb, am, fm, std::false_type{}, std::false_type{});
     }
+    if (more) stage_store(smem + next_buf(cur) * BUF, n1);
     __syncthreads();
-    cur ^= 1;
+    cur = next_buf(cur);
   };
   // Tiles lo, lo+BN, ... < hi, split per wave into three contiguous runs: before the document start of the
   // wave's last query (generic), fully visible from every query of the wave (fast: no mask, no per-subtile test),
@@ -300,9 +479,9 @@ k_fwd(const KParams p) {
   j0 = __builtin_amdgcn_readfirstlane(j0);
   j1 = __builtin_amdgcn_readfirstlane(j1);
   int j = 0;
-  for (; j < j0; ++j) step(lo + j * BN, std::false_type{});
-  for (; j < j1; ++j) step(lo + j * BN, std::true_type{});
-  for (; j < ntile; ++j) step(lo + j * BN, std::false_type{});
+  for (; j < j0; ++j) step(lo + j * BN);
+  if (j < j1) fast_run(j, j1);
+  for (j = j1; j < ntile; ++j) step(lo + j * BN);
 
   T* op = head_ptr_w<T>(p.o, b, hd);
 #pragma unroll
