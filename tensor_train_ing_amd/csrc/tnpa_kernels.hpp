@@ -341,25 +341,34 @@ k_fwd(const KParams p) {
     for (int i = 0; i < KStage::PER; ++i) kvo[pr][i] = KStage::chunk_off(i, kst[pr]);
 #pragma unroll
   for (int i = 0; i < VStage::PER; ++i) vvo[i] = VStage::chunk_off(i, p.v.st);
-  auto stage_load_buf = [&](const int n1) {
+  // part 1: the K rows, part 2: the V rows (issued in different phases so the memory pipe drains in between)
+  auto stage_load_buf = [&](const int n1, const int part) {
     if constexpr (!CHUNKED) return;
+    if (part & 1) {
 #pragma unroll
-    for (int pr = 0; pr < NPAIR; ++pr) {
-      const auto rs = rows_rsrc(kp[pr], kst[pr], n1, DK);
+      for (int pr = 0; pr < NPAIR; ++pr) {
+        const auto rs = rows_rsrc(kp[pr], kst[pr], n1, DK);
 #pragma unroll
-      for (int i = 0; i < KStage::PER; ++i) sk[pr].load_buf(i, rs, kvo[pr][i]);
+        for (int i = 0; i < KStage::PER; ++i) sk[pr].load_buf(i, rs, kvo[pr][i]);
+      }
     }
-    const auto rs = rows_rsrc(vp, p.v.st, n1, DV);
+    if (part & 2) {
+      const auto rs = rows_rsrc(vp, p.v.st, n1, DV);
 #pragma unroll
-    for (int i = 0; i < VStage::PER; ++i) sv.load_buf(i, rs, vvo[i]);
+      for (int i = 0; i < VStage::PER; ++i) sv.load_buf(i, rs, vvo[i]);
+    }
   };
-  auto stage_store_raw = [&](char TNPA_LDS* dstb) {
+  auto stage_store_raw = [&](char TNPA_LDS* dstb, const int part) {
+    if (part & 1) {
 #pragma unroll
-    for (int pr = 0; pr < NPAIR; ++pr)
+      for (int pr = 0; pr < NPAIR; ++pr)
 #pragma unroll
-      for (int i = 0; i < KStage::PER; ++i) sk[pr].store_raw(i, dstb + pr * KTile::BYTES);
+        for (int i = 0; i < KStage::PER; ++i) sk[pr].store_raw(i, dstb + pr * KTile::BYTES);
+    }
+    if (part & 2) {
 #pragma unroll
-    for (int i = 0; i < VStage::PER; ++i) sv.store_raw(i, dstb + NPAIR * KTile::BYTES);
+      for (int i = 0; i < VStage::PER; ++i) sv.store_raw(i, dstb + NPAIR * KTile::BYTES);
+    }
   };
 
   // Run of unmasked tiles jb..je-1 (no mask, no sub-block test).
@@ -367,40 +376,45 @@ k_fwd(const KParams p) {
   // S(g+1) MFMA chain, back to back; phase B(g): O += V^T(g) P(g) MFMAs, with the power of S(g+1) and the K-row
   // reads of g+2 between them. Every operand is read a phase ahead and the VALU work sits between independent
   // MFMAs, so one wave keeps the matrix pipe fed on its own. Tile j+1 is published by the barrier at the start of
-  // B(NKB-2) of tile j, before the first read of its rows; its buffer loads are issued after the previous barrier
-  // and written to LDS in A(NKB-2) (tiles j, j+1 and j+2 in flight). Two buffers: one tile per step, loads
-  // before and stores after the compute.
+  // B(NKB-2) of tile j, before the first read of its rows (tiles j, j+1 and j+2 in flight). Its staging is spread
+  // so the memory pipe and LDS drain between parts: K rows loaded in B(NKB-2) of tile j-1 (after that barrier) and
+  // written in B(NKB-1), V rows loaded in A(NKB-1) and written in A(NKB-2) of tile j. Two buffers: one tile per
+  // step, loads before and stores after the compute.
   auto fast_run = [&](const int jb, const int je) {
     if constexpr (NBUF == 3) {
       Op ka[NPAIR][NCK], vt[NDV][NC2], pop[QW][NC2], pn[QW][NC2];
       f32x16 sn[NPAIR][QW];
-      stage_load_buf(lo + (jb + 1) * BN);  // the step before the run staged only tile jb
+      stage_load_buf(lo + (jb + 1) * BN, 3);  // the step before the run staged only tile jb
       k_rows(ka, smem + cur * BUF, 0);
       s_mma(sn, ka);
       k_rows(ka, smem + cur * BUF, 1);
       power(pop, sn);
+      stage_store_raw(smem + next_buf(cur) * BUF, 1);  // its V rows follow in the first tile's A(NKB-2)
       // one tile; LAST (the run's final tile) drains the pipeline instead of starting the next tile
       auto tile = [&](const int j, auto last_c) {
         constexpr bool LAST = decltype(last_c)::value;
         const int nc = next_buf(cur);
         const char TNPA_LDS* base = smem + cur * BUF;
         char TNPA_LDS* b1 = smem + nc * BUF;
+        char TNPA_LDS* b2 = smem + next_buf(nc) * BUF;
         const int n1 = lo + (j + 1) * BN;
 #pragma unroll
         for (int kb = 0; kb < NKB; ++kb) {
           const bool more_s = kb + 1 < NKB || !LAST;
           v_cols(vt, base, kb);
-          if (kb == NKB - 2) stage_store_raw(b1);
+          if (kb == NKB - 2) stage_store_raw(b1, 2);
+          if (kb == NKB - 1 && !LAST) stage_load_buf(n1 + BN, 2);
           if (more_s) s_mma(sn, ka);
           __builtin_amdgcn_sched_barrier(0);
           if (kb == NKB - 2) {
             __syncthreads();
-            if (!LAST) stage_load_buf(n1 + BN);
+            if (!LAST) stage_load_buf(n1 + BN, 1);
           }
           if (kb + 2 < NKB) k_rows(ka, base, kb + 2);
           else if (!LAST) k_rows(ka, b1, kb + 2 - NKB);
           pv_mma(vt, pop);
           if (more_s) power(pn, sn);
+          if (kb == NKB - 1 && !LAST) stage_store_raw(b2, 1);
           // K-row reads first (a whole phase ahead of their use), then one MFMA per few VALU of the power
           if (kb + 2 < NKB || !LAST) __builtin_amdgcn_sched_group_barrier(0x100, NPAIR * NCK, 0);
 #pragma unroll
