@@ -220,6 +220,17 @@ template <typename T, int ROWS, int D, int WID, int NT> struct Stage {
       }
     }
   }
+  // LDS tile -> global rows row0 + rr for rr < nvalid: the reverse of load() + store(), same coalesced chunks.
+  __device__ inline void copy_out(const char TNPA_LDS* tile, T* __restrict__ g, int64_t st, int row0, int nvalid) const {
+#pragma unroll
+    for (int i = 0; i < PER; ++i) {
+      const int idx = (int)threadIdx.x + i * NT;
+      if (TOTAL % NT == 0 || idx < TOTAL) {
+        const int rr = idx / NCHG, c = idx % NCHG;
+        if (rr < nvalid) *(u32x4*)(g + (int64_t)(row0 + rr) * st + c * CE) = *(const u32x4 TNPA_LDS*)(tile + TL::off(rr, c * CE));
+      }
+    }
+  }
   // Chunk i through a buffer resource over the tile's rows (rows past the resource's end read as zero): one
   // instruction, no address arithmetic or branch, so it can sit between matrix instructions. voff = byte offset of
   // the thread's chunk i inside the tile. Needs TOTAL % NT == 0.
@@ -251,6 +262,124 @@ template <typename T, int ROWS, int D, int WID, int NT> struct Stage {
         u32x4{ok ? r[i][0] : 0u, ok ? r[i][1] : 0u, ok ? r[i][2] : 0u, ok ? r[i][3] : 0u};
   }
 };
+
+// Buffer resource over rows n1.. of one (b, h) head of row stride st (elements) and D real columns: rows at or
+// past T read as zero (the hardware range check), so staged tiles need no clamp or select.
+template <typename T>
+__device__ inline __amdgpu_buffer_rsrc_t rows_rsrc(const T* base, int64_t st, int n1, int T_, int D) {
+  const int64_t rem = n1 < T_ ? ((int64_t)(T_ - 1 - n1) * st + D) * (int64_t)sizeof(T) : 0;
+  const int nrec = (int)(rem < 0x7fffffff ? rem : 0x7fffffff);
+  return __builtin_amdgcn_make_buffer_rsrc((void*)(base + (int64_t)n1 * st), (short)0, nrec, 0x00020000);
+}
+
+// Staging of one streamed tile made of NA tiles of DA columns (part 1) and one tile of DB columns (part 2),
+// through buffer loads into registers and 16-byte LDS stores, in two independently placed parts. In LDS the
+// A tiles sit at buf + i * TA::BYTES and the B tile after them.
+template <typename T, int ROWS, int DA, int DAP, int DB, int DBP, int NT, int NA> struct PartStager {
+  typedef Stage<T, ROWS, DA, DAP, NT> SA;
+  typedef Stage<T, ROWS, DB, DBP, NT> SB;
+  typedef Tile<T, ROWS, DAP> TA;
+  static constexpr bool OK = SA::TOTAL % NT == 0 && SB::TOTAL % NT == 0;
+  SA sa[NA];
+  SB sb;
+  uint32_t oa[NA][SA::PER], ob[SB::PER];
+  const T* pa[NA];
+  const T* pb;
+  int64_t sta[NA], stb;
+  int T_;
+  const float* bscale = nullptr;  // optional per-row factor applied to the B rows when they are written to LDS
+  float fb[SB::PER];
+
+  __device__ inline void init(const T* const* a, const int64_t* ast, const T* b, int64_t bst, int nrows) {
+#pragma unroll
+    for (int i = 0; i < NA; ++i) {
+      pa[i] = a[i];
+      sta[i] = ast[i];
+#pragma unroll
+      for (int k = 0; k < SA::PER; ++k) oa[i][k] = SA::chunk_off(k, ast[i]);
+    }
+    pb = b;
+    stb = bst;
+#pragma unroll
+    for (int k = 0; k < SB::PER; ++k) ob[k] = SB::chunk_off(k, bst);
+    T_ = nrows;
+  }
+  // The same, one 16-byte chunk per thread at a time: parts 0 .. NPARTS-1, A chunks first.
+  static constexpr int NPARTS = NA * SA::PER + SB::PER;
+  __device__ inline void load_part(int q, int n1) {
+    if (q < NA * SA::PER) {
+      const int i = q / SA::PER, k = q % SA::PER;
+      sa[i].load_buf(k, rows_rsrc<T>(pa[i], sta[i], n1, T_, DA), oa[i][k]);
+    } else {
+      const int k = q - NA * SA::PER;
+      sb.load_buf(k, rows_rsrc<T>(pb, stb, n1, T_, DB), ob[k]);
+      if (bscale != nullptr) {
+        const int row = n1 + ((int)threadIdx.x + k * NT) / SB::NCHG;
+        fb[k] = row < T_ ? bscale[row] : 0.f;
+      }
+    }
+  }
+  __device__ inline void store_part(int q, char TNPA_LDS* buf) const {
+    if (q < NA * SA::PER) {
+      const int i = q / SA::PER, k = q % SA::PER;
+      sa[i].store_raw(k, buf + i * TA::BYTES);
+    } else {
+      const int k = q - NA * SA::PER;
+      if (bscale == nullptr) {
+        sb.store_raw(k, buf + NA * TA::BYTES);
+      } else {  // same product and rounding as Stage::load_scaled
+        SB t;
+        t.r[k] = sb.r[k];
+        if constexpr (sizeof(T) == 2) {
+          T* e = reinterpret_cast<T*>(&t.r[k]);
+#pragma unroll
+          for (int j = 0; j < 8; ++j) e[j] = (T)((float)e[j] * fb[k]);
+        } else {
+          float* e = reinterpret_cast<float*>(&t.r[k]);
+#pragma unroll
+          for (int j = 0; j < 4; ++j) e[j] *= fb[k];
+        }
+        t.store_raw(k, buf + NA * TA::BYTES);
+      }
+    }
+  }
+  // rows n1 .. n1 + ROWS - 1 into registers / registers into an LDS buffer: part 1 = the A tiles, 2 = the B tile
+  __device__ inline void load(int part, int n1) {
+#pragma unroll
+    for (int q = 0; q < NPARTS; ++q)
+      if (part & (q < NA * SA::PER ? 1 : 2)) load_part(q, n1);
+  }
+  __device__ inline void store(int part, char TNPA_LDS* buf) const {
+#pragma unroll
+    for (int q = 0; q < NPARTS; ++q)
+      if (part & (q < NA * SA::PER ? 1 : 2)) store_part(q, buf);
+  }
+};
+
+// One wave's 32-row accumulator block -> rows rbase .. rbase + 31 of an LDS tile of T: lane (l32, h) holds, for
+// row rbase + l32, columns 32 d + 8 g + 4 h + (0..3) in acc[d][4 g + (0..3)]; each is scaled by f and rounded to T.
+// Columns at or past ncol are not written. Used to turn the per-lane output layout into coalesced row stores.
+template <typename T, typename TL, int ND>
+__device__ inline void acc_rows_to_lds(char TNPA_LDS* tile, int rbase, int l32, int h, const f32x16 (&acc)[ND], float f,
+                                       int ncol) {
+#pragma unroll
+  for (int d = 0; d < ND; ++d)
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+      const int col = 32 * d + 8 * g + 4 * h;
+      if (col >= ncol) continue;
+      char TNPA_LDS* q = tile + TL::off(rbase + l32, col);
+      if constexpr (sizeof(T) == 2) {
+        typedef T T4 __attribute__((ext_vector_type(4)));
+        T4 v;
+        v[0] = (T)(acc[d][4 * g] * f); v[1] = (T)(acc[d][4 * g + 1] * f);
+        v[2] = (T)(acc[d][4 * g + 2] * f); v[3] = (T)(acc[d][4 * g + 3] * f);
+        *(T4 TNPA_LDS*)q = v;
+      } else {
+        *(f32x4 TNPA_LDS*)q = f32x4{acc[d][4 * g] * f, acc[d][4 * g + 1] * f, acc[d][4 * g + 2] * f, acc[d][4 * g + 3] * f};
+      }
+    }
+}
 
 // Stores 4 consecutive output elements (one accumulator register group) converted to T.
 template <typename T> __device__ inline void store4(T* __restrict__ p, float a, float b, float c, float d) {

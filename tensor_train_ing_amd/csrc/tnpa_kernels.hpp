@@ -107,6 +107,8 @@ template <typename T> __device__ inline T* head_ptr_w(const TDesc& d, int b, int
   return (T*)d.p + (int64_t)b * d.sb + (int64_t)hd * d.sh;
 }
 
+__host__ __device__ constexpr int cmax(int a, int b) { return a > b ? a : b; }
+
 // ------------------------------------------------------------------------------------------------ tile configs
 // NW waves per workgroup, QW / KW 32-row subtiles per wave, BN / BM rows per LDS tile, WPE = waves per SIMD the
 // register allocation must allow (2 lets a second wave hide the first one's LDS latency).
@@ -140,7 +142,14 @@ k_fwd(const KParams p) {
   // three tile buffers for the pipelined unmasked run when they fit the 160 KB of LDS, else two
   constexpr bool CHUNKED = Stage<T, BN, DK, DKP, NT>::TOTAL % NT == 0 && Stage<T, BN, DV, DVP, NT>::TOTAL % NT == 0;
   constexpr int NBUF = CHUNKED && NKB >= 2 && 3 * BUF <= 160 * 1024 ? 3 : 2;
-  __shared__ __attribute__((aligned(16))) char smem_[NBUF * BUF];
+  // The block's Q rows come in, and its O rows go out, through LDS as whole coalesced rows (ROWLDS; not with
+  // zero-padded head dims, whose pad columns in the tile buffers must stay zero).
+  typedef Tile<T, BM, DKP> QTile;
+  typedef Tile<T, BM, DVP> OTile;
+  constexpr bool ROWLDS = DKP == DK && DVP == DV && NPAIR * QTile::BYTES <= 160 * 1024;
+  constexpr int SMEM = cmax(NBUF * BUF, cmax(ROWLDS ? NPAIR * QTile::BYTES : 0, OTile::BYTES));
+  static_assert(SMEM <= 160 * 1024, "LDS");
+  __shared__ __attribute__((aligned(16))) char smem_[SMEM];
   char TNPA_LDS* smem = (char TNPA_LDS*)smem_;
 
   const int T_ = p.T, BH = p.B * p.H;
@@ -159,7 +168,7 @@ k_fwd(const KParams p) {
   const float* rsc = p.rscale + (int64_t)b * T_;
 
   if constexpr (DKP != DK || DVP != DV) {
-    for (int i = threadIdx.x; i < NBUF * BUF / 16; i += NT) ((u32x4 TNPA_LDS*)smem)[i] = u32x4{0u, 0u, 0u, 0u};
+    for (int i = threadIdx.x; i < SMEM / 16; i += NT) ((u32x4 TNPA_LDS*)smem)[i] = u32x4{0u, 0u, 0u, 0u};
     __syncthreads();
   }
 
@@ -177,10 +186,28 @@ k_fwd(const KParams p) {
     const bool valid = q < T_;
     dsq[s] = valid ? dst[q] : INT_MAX;
     scq[s] = valid ? rsc[q] : 0.f;
+    if constexpr (!ROWLDS) {
+#pragma unroll
+      for (int pr = 0; pr < NPAIR; ++pr)
+#pragma unroll
+        for (int c = 0; c < NCK; ++c) qf[pr][s][c] = valid ? load_op<T>(qp[pr] + (int64_t)q * qst[pr], c, h) : M::zero();
+    }
+  }
+  if constexpr (ROWLDS) {
+    Stage<T, BM, DK, DKP, NT> qs[NPAIR];
+#pragma unroll
+    for (int pr = 0; pr < NPAIR; ++pr) qs[pr].load(qp[pr], qst[pr], m0, T_ - m0);
+#pragma unroll
+    for (int pr = 0; pr < NPAIR; ++pr) qs[pr].store(smem + pr * QTile::BYTES);
+    __syncthreads();
 #pragma unroll
     for (int pr = 0; pr < NPAIR; ++pr)
 #pragma unroll
-      for (int c = 0; c < NCK; ++c) qf[pr][s][c] = valid ? load_op<T>(qp[pr] + (int64_t)q * qst[pr], c, h) : M::zero();
+      for (int s = 0; s < QW; ++s)
+#pragma unroll
+        for (int c = 0; c < NCK; ++c)
+          qf[pr][s][c] = read_row<T, QTile>(smem + pr * QTile::BYTES, 32 * (wave * QW + s), l32, c, h);
+    __syncthreads();
   }
 
   f32x16 oacc[QW][NDV];
@@ -497,23 +524,14 @@ k_fwd(const KParams p) {
   if (j < j1) fast_run(j, j1);
   for (j = j1; j < ntile; ++j) step(lo + j * BN);
 
+  // O rows: scaled in registers, gathered in LDS, written as whole rows
   T* op = head_ptr_w<T>(p.o, b, hd);
+  __syncthreads();  // every wave is done with the tile buffers
 #pragma unroll
-  for (int s = 0; s < QW; ++s) {
-    const int q = qa[s] + l32;
-    if (q >= T_) continue;
-    const float f = scq[s] * p.vf;
-    T* row = op + (int64_t)q * p.o.st;
-#pragma unroll
-    for (int d = 0; d < NDV; ++d)
-#pragma unroll
-      for (int g = 0; g < 4; ++g) {
-        const int col = 32 * d + 8 * g + 4 * h;
-        if (col < DV)
-          store4<T>(row + col, oacc[s][d][4 * g] * f, oacc[s][d][4 * g + 1] * f, oacc[s][d][4 * g + 2] * f,
-                    oacc[s][d][4 * g + 3] * f);
-      }
-  }
+  for (int s = 0; s < QW; ++s) acc_rows_to_lds<T, OTile, NDV>(smem, 32 * (wave * QW + s), l32, h, oacc[s], scq[s] * p.vf, DV);
+  __syncthreads();
+  Stage<T, BM, DV, DVP, NT> os;
+  os.copy_out(smem, op, p.o.st, m0, T_ - m0);
 }
 
 // ------------------------------------------------------------------------------------------------ dQ
@@ -531,7 +549,18 @@ k_bwd_q(const KParams p) {
   typedef Tile<T, BN, DKP> KTile;
   typedef Tile<T, BN, DVP> VTile;
   constexpr int BUF = NPAIR * KTile::BYTES + VTile::BYTES;
-  __shared__ __attribute__((aligned(16))) char smem_[2 * BUF];
+  typedef PartStager<T, BN, DK, DKP, DV, DVP, NT, NPAIR> Stager;
+  // three tile buffers (each tile staged over two steps, its parts in different sub-blocks) when they fit the
+  // 160 KB of LDS and the tile splits evenly over the threads, else two
+  constexpr int NBUF = Stager::OK && NKB >= 2 && 3 * BUF <= 160 * 1024 ? 3 : 2;
+  // The block's Q and dO rows come in, and its dQ rows go out, through LDS as whole coalesced rows (ROWLDS; not
+  // with zero-padded head dims, whose pad columns in the tile buffers must stay zero).
+  typedef Tile<T, BM, DKP> QTile;
+  typedef Tile<T, BM, DVP> DOTile;
+  constexpr bool ROWLDS = DKP == DK && DVP == DV && NPAIR * QTile::BYTES + DOTile::BYTES <= 160 * 1024;
+  constexpr int SMEM = cmax(NBUF * BUF, cmax(ROWLDS ? NPAIR * QTile::BYTES + DOTile::BYTES : 0, QTile::BYTES));
+  static_assert(SMEM <= 160 * 1024, "LDS");
+  __shared__ __attribute__((aligned(16))) char smem_[SMEM];
   char TNPA_LDS* smem = (char TNPA_LDS*)smem_;
 
   const int T_ = p.T, BH = p.B * p.H;
@@ -551,7 +580,7 @@ k_bwd_q(const KParams p) {
   const float* rsc = p.rscale + (int64_t)b * T_;
 
   if constexpr (DKP != DK || DVP != DV) {
-    for (int i = threadIdx.x; i < 2 * BUF / 16; i += NT) ((u32x4 TNPA_LDS*)smem)[i] = u32x4{0u, 0u, 0u, 0u};
+    for (int i = threadIdx.x; i < SMEM / 16; i += NT) ((u32x4 TNPA_LDS*)smem)[i] = u32x4{0u, 0u, 0u, 0u};
     __syncthreads();
   }
 
@@ -570,12 +599,37 @@ k_bwd_q(const KParams p) {
     const bool valid = q < T_;
     dsq[s] = valid ? dst[q] : INT_MAX;
     scq[s] = valid ? rsc[q] : 0.f;
+    if constexpr (!ROWLDS) {
 #pragma unroll
-    for (int pr = 0; pr < NPAIR; ++pr)
+      for (int pr = 0; pr < NPAIR; ++pr)
 #pragma unroll
-      for (int c = 0; c < NCK; ++c) qf[pr][s][c] = valid ? load_op<T>(qp[pr] + (int64_t)q * qst[pr], c, h) : M::zero();
+        for (int c = 0; c < NCK; ++c) qf[pr][s][c] = valid ? load_op<T>(qp[pr] + (int64_t)q * qst[pr], c, h) : M::zero();
 #pragma unroll
-    for (int c = 0; c < NCV; ++c) dof[s][c] = valid ? load_op<T>(dop + (int64_t)q * p.dout.st, c, h) : M::zero();
+      for (int c = 0; c < NCV; ++c) dof[s][c] = valid ? load_op<T>(dop + (int64_t)q * p.dout.st, c, h) : M::zero();
+    }
+  }
+  if constexpr (ROWLDS) {
+    Stage<T, BM, DK, DKP, NT> qs[NPAIR];
+    Stage<T, BM, DV, DVP, NT> ds;
+#pragma unroll
+    for (int pr = 0; pr < NPAIR; ++pr) qs[pr].load(qp[pr], qst[pr], m0, T_ - m0);
+    ds.load(dop, p.dout.st, m0, T_ - m0);
+#pragma unroll
+    for (int pr = 0; pr < NPAIR; ++pr) qs[pr].store(smem + pr * QTile::BYTES);
+    ds.store(smem + NPAIR * QTile::BYTES);
+    __syncthreads();
+#pragma unroll
+    for (int s = 0; s < QW; ++s) {
+#pragma unroll
+      for (int pr = 0; pr < NPAIR; ++pr)
+#pragma unroll
+        for (int c = 0; c < NCK; ++c)
+          qf[pr][s][c] = read_row<T, QTile>(smem + pr * QTile::BYTES, 32 * (wave * QW + s), l32, c, h);
+#pragma unroll
+      for (int c = 0; c < NCV; ++c)
+        dof[s][c] = read_row<T, DOTile>(smem + NPAIR * QTile::BYTES, 32 * (wave * QW + s), l32, c, h);
+    }
+    __syncthreads();
   }
 
   f32x16 dq[NPAIR][QW][NDK];
@@ -590,16 +644,27 @@ k_bwd_q(const KParams p) {
   const int hi = min(m0 + BM, T_);
   Stage<T, BN, DK, DKP, NT> sk[NPAIR];
   Stage<T, BN, DV, DVP, NT> sv;
+  Stager stg;
+  if constexpr (NBUF == 3) {
+    stg.init(kp, kst, vp, p.v.st, T_);
+    stg.load(3, lo);
+    stg.store(3, smem);
+    stg.load(3, lo + BN);
+  } else {
 #pragma unroll
-  for (int pr = 0; pr < NPAIR; ++pr) sk[pr].load(kp[pr], kst[pr], lo, T_ - lo);
-  sv.load(vp, p.v.st, lo, T_ - lo);
+    for (int pr = 0; pr < NPAIR; ++pr) sk[pr].load(kp[pr], kst[pr], lo, T_ - lo);
+    sv.load(vp, p.v.st, lo, T_ - lo);
 #pragma unroll
-  for (int pr = 0; pr < NPAIR; ++pr) sk[pr].store(smem + pr * KTile::BYTES);
-  sv.store(smem + NPAIR * KTile::BYTES);
+    for (int pr = 0; pr < NPAIR; ++pr) sk[pr].store(smem + pr * KTile::BYTES);
+    sv.store(smem + NPAIR * KTile::BYTES);
+  }
   __syncthreads();
+  auto next_buf = [](const int c) { return c + 1 == NBUF ? 0 : c + 1; };
 
   int cur = 0;
-  auto sub = [&](const char TNPA_LDS* base, const int n0, const int kb, const uint32_t am, const uint32_t fm, auto all_c, auto full_c) {
+  // mid: work placed between the sub-block's S/dP MFMA chains and its VALU (the spread tile staging)
+  auto sub = [&](const char TNPA_LDS* base, const int n0, const int kb, const uint32_t am, const uint32_t fm, auto all_c, auto full_c,
+                 auto&& mid) {
     constexpr bool ALL = decltype(all_c)::value, FULL = decltype(full_c)::value;
     const int key0 = n0 + 32 * kb;
     f32x16 sacc[NPAIR][QW], pacc[QW];
@@ -625,6 +690,7 @@ k_bwd_q(const KParams p) {
       for (int s = 0; s < QW; ++s)
         if (ALL || ((am >> s) & 1u)) pacc[s] = M::mma(a, dof[s][c], pacc[s]);
     }
+    mid();
     Op dso[NPAIR][QW][NC2];
 #pragma unroll
     for (int s = 0; s < QW; ++s) {
@@ -668,7 +734,22 @@ k_bwd_q(const KParams p) {
   // prefetched tile into the other buffer, one barrier.
   auto step = [&](const int n0, auto fast_c) {
     constexpr bool FAST = decltype(fast_c)::value;
-    const bool more = n0 + BN < hi;
+    const bool more = NBUF == 2 && n0 + BN < hi;
+    // three buffers: tile j+1 (in registers since the previous step) is written to its buffer and tile j+2 loaded
+    // in its place, one 16-byte chunk per thread at each of 2 * NKB points (the middle and the end of every
+    // sub-block), so that the loads of all waves reach the memory pipe spread over the step
+    char TNPA_LDS* b1 = smem + next_buf(cur) * BUF;
+    auto stage_at = [&](const int point) {
+      if constexpr (NBUF == 3) {
+#pragma unroll
+        for (int q = 0; q < Stager::NPARTS; ++q)
+          if (q % (2 * NKB) == point) {
+            stg.store_part(q, b1);
+            stg.load_part(q, n0 + 2 * BN);
+          }
+      }
+    };
+    auto mid_for = [&](const int kb) { return [&, kb]() { stage_at(2 * kb); }; };
     if (more) {
 #pragma unroll
       for (int pr = 0; pr < NPAIR; ++pr) sk[pr].load(kp[pr], kst[pr], n0 + BN, T_ - n0 - BN);
@@ -677,7 +758,10 @@ k_bwd_q(const KParams p) {
     const char TNPA_LDS* base = smem + cur * BUF;
     if constexpr (FAST) {
 #pragma unroll
-      for (int kb = 0; kb < NKB; ++kb) sub(base, n0, kb, 0u, 0u, std::true_type{}, std::true_type{});
+      for (int kb = 0; kb < NKB; ++kb) {
+        sub(base, n0, kb, 0u, 0u, std::true_type{}, std::true_type{}, mid_for(kb));
+        stage_at(2 * kb + 1);
+      }
     } else {
 #pragma unroll
       for (int kb = 0; kb < NKB; ++kb) {
@@ -690,18 +774,19 @@ k_bwd_q(const KParams p) {
         }
         am = __builtin_amdgcn_readfirstlane(am);
         fm = __builtin_amdgcn_readfirstlane(fm);
+        stage_at(2 * kb);  // outside the skip test: one code path, so no wait on the loads it issues
+        stage_at(2 * kb + 1);
         if (am == 0) continue;
-        sub(base, n0, kb, am, fm, std::false_type{}, std::false_type{});
+        sub(base, n0, kb, am, fm, std::false_type{}, std::false_type{}, [] {});
       }
     }
     if (more) {
-      char TNPA_LDS* nxt = smem + (cur ^ 1) * BUF;
 #pragma unroll
-      for (int pr = 0; pr < NPAIR; ++pr) sk[pr].store(nxt + pr * KTile::BYTES);
-      sv.store(nxt + NPAIR * KTile::BYTES);
+      for (int pr = 0; pr < NPAIR; ++pr) sk[pr].store(b1 + pr * KTile::BYTES);
+      sv.store(b1 + NPAIR * KTile::BYTES);
     }
     __syncthreads();
-    cur ^= 1;
+    cur = next_buf(cur);
   };
   // Tiles lo, lo+BN, ... < hi, split per wave into three contiguous runs: before the document start of the
   // wave's last query (generic), fully visible from every query of the wave (fast: no mask, no per-subtile test),
@@ -720,26 +805,17 @@ k_bwd_q(const KParams p) {
   for (; j < j1; ++j) step(lo + j * BN, std::true_type{});
   for (; j < ntile; ++j) step(lo + j * BN, std::false_type{});
 
+  // dQ rows: scaled in registers, gathered in LDS, written as whole rows
   const TDesc* outs[2] = {&p.dq1, &p.dq2};
 #pragma unroll
   for (int pr = 0; pr < NPAIR; ++pr) {
-    T* dqp = head_ptr_w<T>(*outs[pr], b, hd);
+    __syncthreads();  // every wave is done with the tile buffers (or with the previous pair's rows)
 #pragma unroll
-    for (int s = 0; s < QW; ++s) {
-      const int q = qa[s] + l32;
-      if (q >= T_) continue;
-      const float f = scq[s] * p.gf;
-      T* row = dqp + (int64_t)q * outs[pr]->st;
-#pragma unroll
-      for (int d = 0; d < NDK; ++d)
-#pragma unroll
-        for (int g = 0; g < 4; ++g) {
-          const int col = 32 * d + 8 * g + 4 * h;
-          if (col < DK)
-            store4<T>(row + col, dq[pr][s][d][4 * g] * f, dq[pr][s][d][4 * g + 1] * f, dq[pr][s][d][4 * g + 2] * f,
-                      dq[pr][s][d][4 * g + 3] * f);
-        }
-    }
+    for (int s = 0; s < QW; ++s)
+      acc_rows_to_lds<T, QTile, NDK>(smem, 32 * (wave * QW + s), l32, h, dq[pr][s], scq[s] * p.gf, DK);
+    __syncthreads();
+    Stage<T, BM, DK, DKP, NT> os;
+    os.copy_out(smem, head_ptr_w<T>(*outs[pr], b, hd), outs[pr]->st, m0, T_ - m0);
   }
 }
 
@@ -764,7 +840,19 @@ k_bwd_kv(const KParams p) {
   typedef Tile<T, BMQ, DKP> QTile;
   typedef Tile<T, BMQ, DVP> OTile;
   constexpr int BUF = NPAIR * QTile::BYTES + OTile::BYTES + BMQ * 4;
-  __shared__ __attribute__((aligned(16))) char smem_[2 * BUF];
+  typedef PartStager<T, BMQ, DK, DKP, DV, DVP, NT, NPAIR> Stager;
+  // three tile buffers (each query tile staged over two steps, one chunk per thread at a time) when they fit the
+  // 160 KB of LDS and the tile splits evenly over the threads, else two (and for the two-pair kinds, whose single
+  // key-side kernel is already short of registers)
+  constexpr int NBUF = Stager::OK && NPAIR == 1 && NQB >= 2 && 3 * BUF <= 160 * 1024 ? 3 : 2;
+  // The block's K and V rows come in, and its dK / dV rows go out, through LDS as whole coalesced rows (ROWLDS;
+  // not with zero-padded head dims, whose pad columns in the tile buffers must stay zero).
+  typedef Tile<T, BNK, DKP> KRows;
+  typedef Tile<T, BNK, DVP> VRows;
+  constexpr bool ROWLDS = DKP == DK && DVP == DV && NPAIR == 1 && KRows::BYTES + VRows::BYTES <= 160 * 1024 - 16 * NW;
+  constexpr int SMEM = cmax(NBUF * BUF, cmax(ROWLDS ? NPAIR * KRows::BYTES + VRows::BYTES : 0, cmax(KRows::BYTES, VRows::BYTES)));
+  static_assert(SMEM <= 160 * 1024 - 16 * NW, "LDS");
+  __shared__ __attribute__((aligned(16))) char smem_[SMEM];
   __shared__ float red_[NW][4];
   char TNPA_LDS* smem = (char TNPA_LDS*)smem_;
 
@@ -785,7 +873,7 @@ k_bwd_kv(const KParams p) {
   const float* rsc = p.rscale + (int64_t)b * T_;
 
   if constexpr (DKP != DK || DVP != DV) {
-    for (int i = threadIdx.x; i < 2 * BUF / 16; i += NT) ((u32x4 TNPA_LDS*)smem)[i] = u32x4{0u, 0u, 0u, 0u};
+    for (int i = threadIdx.x; i < SMEM / 16; i += NT) ((u32x4 TNPA_LDS*)smem)[i] = u32x4{0u, 0u, 0u, 0u};
     __syncthreads();
   }
 
@@ -798,12 +886,36 @@ k_bwd_kv(const KParams p) {
     ka[s] = nw0 + 32 * s;
     const int key = ka[s] + l32;
     const bool valid = key < T_;
+    if constexpr (!ROWLDS) {
 #pragma unroll
-    for (int pr = 0; pr < NPAIR; ++pr)
+      for (int pr = 0; pr < NPAIR; ++pr)
 #pragma unroll
-      for (int c = 0; c < NCK; ++c) kf[pr][s][c] = valid ? load_op<T>(kp[pr] + (int64_t)key * kst[pr], c, h) : M::zero();
+        for (int c = 0; c < NCK; ++c) kf[pr][s][c] = valid ? load_op<T>(kp[pr] + (int64_t)key * kst[pr], c, h) : M::zero();
 #pragma unroll
-    for (int c = 0; c < NCV; ++c) vf[s][c] = valid ? load_op<T>(vp + (int64_t)key * p.v.st, c, h) : M::zero();
+      for (int c = 0; c < NCV; ++c) vf[s][c] = valid ? load_op<T>(vp + (int64_t)key * p.v.st, c, h) : M::zero();
+    }
+  }
+  if constexpr (ROWLDS) {
+    Stage<T, BNK, DK, DKP, NT> ks[NPAIR];
+    Stage<T, BNK, DV, DVP, NT> vs;  // V only feeds dP (dK pass)
+#pragma unroll
+    for (int pr = 0; pr < NPAIR; ++pr) ks[pr].load(kp[pr], kst[pr], n0, T_ - n0);
+    if constexpr (WANT_DK) vs.load(vp, p.v.st, n0, T_ - n0);
+#pragma unroll
+    for (int pr = 0; pr < NPAIR; ++pr) ks[pr].store(smem + pr * KRows::BYTES);
+    if constexpr (WANT_DK) vs.store(smem + NPAIR * KRows::BYTES);
+    __syncthreads();
+#pragma unroll
+    for (int s = 0; s < KW; ++s) {
+#pragma unroll
+      for (int pr = 0; pr < NPAIR; ++pr)
+#pragma unroll
+        for (int c = 0; c < NCK; ++c) kf[pr][s][c] = read_row<T, KRows>(smem + pr * KRows::BYTES, 32 * (wave * KW + s), l32, c, h);
+#pragma unroll
+      for (int c = 0; c < (WANT_DK ? NCV : 0); ++c)
+        vf[s][c] = read_row<T, VRows>(smem + NPAIR * KRows::BYTES, 32 * (wave * KW + s), l32, c, h);
+    }
+    __syncthreads();
   }
 
   f32x16 dk[NPAIR][KW][NDK], dv[KW][NDV];
@@ -823,23 +935,45 @@ k_bwd_kv(const KParams p) {
   Stage<T, BMQ, DK, DKP, NT> sq[NPAIR];
   Stage<T, BMQ, DV, DVP, NT> so;
   constexpr int DSOFF = NPAIR * QTile::BYTES + OTile::BYTES;
-#pragma unroll
-  for (int pr = 0; pr < NPAIR; ++pr) sq[pr].load(qp[pr], qst[pr], qlo, T_ - qlo);
   const T* dscp = head_ptr<T>(p.dsc, b, hd);
-  if (p.dpre) so.load(dscp, p.dsc.st, qlo, T_ - qlo);
-  else so.load_scaled(dop, p.dout.st, qlo, T_ - qlo, rsc);
+  auto ds_of = [&](const int m) { return m + (int)threadIdx.x < T_ ? dst[m + threadIdx.x] : INT_MAX; };
   int dsv = 0;
-  if (threadIdx.x < BMQ) dsv = qlo + (int)threadIdx.x < T_ ? dst[qlo + threadIdx.x] : INT_MAX;
+  Stager stg;
+  if constexpr (NBUF == 3) {
+    // dO' rows: pre-scaled by the caller, or scaled here when written to LDS
+    if (p.dpre) {
+      stg.init(qp, qst, dscp, p.dsc.st, T_);
+    } else {
+      stg.init(qp, qst, dop, p.dout.st, T_);
+      stg.bscale = rsc;
+    }
+    stg.load(3, qlo);
+    if (threadIdx.x < BMQ) dsv = ds_of(qlo);
 #pragma unroll
-  for (int pr = 0; pr < NPAIR; ++pr) sq[pr].store(smem + pr * QTile::BYTES);
-  so.store(smem + NPAIR * QTile::BYTES);
-  if (threadIdx.x < BMQ) ((int TNPA_LDS*)(smem + DSOFF))[threadIdx.x] = dsv;
+    for (int q = 0; q < Stager::NPARTS; ++q) stg.store_part(q, smem);
+    if (threadIdx.x < BMQ) ((int TNPA_LDS*)(smem + DSOFF))[threadIdx.x] = dsv;
+    stg.load(3, qlo + BMQ);
+    if (threadIdx.x < BMQ) dsv = ds_of(qlo + BMQ);
+  } else {
+#pragma unroll
+    for (int pr = 0; pr < NPAIR; ++pr) sq[pr].load(qp[pr], qst[pr], qlo, T_ - qlo);
+    if (p.dpre) so.load(dscp, p.dsc.st, qlo, T_ - qlo);
+    else so.load_scaled(dop, p.dout.st, qlo, T_ - qlo, rsc);
+    if (threadIdx.x < BMQ) dsv = ds_of(qlo);
+#pragma unroll
+    for (int pr = 0; pr < NPAIR; ++pr) sq[pr].store(smem + pr * QTile::BYTES);
+    so.store(smem + NPAIR * QTile::BYTES);
+    if (threadIdx.x < BMQ) ((int TNPA_LDS*)(smem + DSOFF))[threadIdx.x] = dsv;
+  }
   __syncthreads();
+  auto next_buf = [](const int c) { return c + 1 == NBUF ? 0 : c + 1; };
 
   int cur = 0;
   // One 32-query sub-block for this wave. am / fm: wave-uniform bitmasks of the key subtiles seen by any query of
   // the sub-block / seen by all of them.
-  auto sub = [&](const char TNPA_LDS* base, const int TNPA_LDS* dsl, const int m, const int qb, const uint32_t am, const uint32_t fm, auto all_c, auto full_c) {
+  // mid: work placed between the sub-block's S/dP MFMA chains and its VALU (the spread tile staging)
+  auto sub = [&](const char TNPA_LDS* base, const int TNPA_LDS* dsl, const int m, const int qb, const uint32_t am, const uint32_t fm, auto all_c, auto full_c,
+                 auto&& mid) {
     constexpr bool ALL = decltype(all_c)::value, FULL = decltype(full_c)::value;
     f32x16 sacc[NPAIR][KW], pacc[KW];
 #pragma unroll
@@ -866,6 +1000,7 @@ k_bwd_kv(const KParams p) {
           if (ALL || ((am >> s) & 1u)) pacc[s] = M::mma(a, vf[s][c], pacc[s]);
       }
     }
+    mid();
     Op po[KW][NC2];
     Op dso[NPAIR][KW][NC2];
 #pragma unroll
@@ -928,22 +1063,46 @@ k_bwd_kv(const KParams p) {
 
   auto step = [&](const int m, auto fast_c) {
     constexpr bool FAST = decltype(fast_c)::value;
-    const bool more = m + BMQ < qhi;
+    const bool more = NBUF == 2 && m + BMQ < qhi;
+    // three buffers: tile j+1 (in registers since the previous step) is written to its buffer and tile j+2 loaded
+    // in its place, one 16-byte chunk per thread at each of 2 * NQB points (the middle and the end of every
+    // sub-block), so that the loads of all waves reach the memory pipe spread over the step
+    char TNPA_LDS* b1 = smem + next_buf(cur) * BUF;
+    auto stage_at = [&](const int point) {
+      if constexpr (NBUF == 3) {
+#pragma unroll
+        for (int q = 0; q < Stager::NPARTS; ++q)
+          if (q % (2 * NQB) == point) {
+            stg.store_part(q, b1);
+            stg.load_part(q, m + 2 * BMQ);
+          }
+        if (point == 0 && threadIdx.x < BMQ) {
+          ((int TNPA_LDS*)(b1 + DSOFF))[threadIdx.x] = dsv;
+          dsv = ds_of(m + 2 * BMQ);
+        }
+      }
+    };
+    auto mid_for = [&](const int qb) { return [&, qb]() { stage_at(2 * qb); }; };
     if (more) {
 #pragma unroll
       for (int pr = 0; pr < NPAIR; ++pr) sq[pr].load(qp[pr], qst[pr], m + BMQ, T_ - m - BMQ);
       if (p.dpre) so.load(dscp, p.dsc.st, m + BMQ, T_ - m - BMQ);
       else so.load_scaled(dop, p.dout.st, m + BMQ, T_ - m - BMQ, rsc);
-      if (threadIdx.x < BMQ) dsv = m + BMQ + (int)threadIdx.x < T_ ? dst[m + BMQ + threadIdx.x] : INT_MAX;
+      if (threadIdx.x < BMQ) dsv = ds_of(m + BMQ);
     }
     const char TNPA_LDS* base = smem + cur * BUF;
     const int TNPA_LDS* dsl = (const int TNPA_LDS*)(base + DSOFF);
     if constexpr (FAST) {
 #pragma unroll
-      for (int qb = 0; qb < NQB; ++qb) sub(base, dsl, m, qb, 0u, 0u, std::true_type{}, std::true_type{});
+      for (int qb = 0; qb < NQB; ++qb) {
+        sub(base, dsl, m, qb, 0u, 0u, std::true_type{}, std::true_type{}, mid_for(qb));
+        stage_at(2 * qb + 1);
+      }
     } else {
 #pragma unroll
       for (int qb = 0; qb < NQB; ++qb) {
+        stage_at(2 * qb);  // outside the skip tests: one code path, so no wait on the loads it issues
+        stage_at(2 * qb + 1);
         const int q0 = m + 32 * qb;
         if (q0 >= T_) continue;
         const int qlast = min(q0 + 31, T_ - 1);
@@ -957,18 +1116,17 @@ k_bwd_kv(const KParams p) {
         am = __builtin_amdgcn_readfirstlane(am);
         fm = __builtin_amdgcn_readfirstlane(fm);
         if (am == 0) continue;
-        sub(base, dsl, m, qb, am, fm, std::false_type{}, std::false_type{});
+        sub(base, dsl, m, qb, am, fm, std::false_type{}, std::false_type{}, [] {});
       }
     }
     if (more) {
-      char TNPA_LDS* nxt = smem + (cur ^ 1) * BUF;
 #pragma unroll
-      for (int pr = 0; pr < NPAIR; ++pr) sq[pr].store(nxt + pr * QTile::BYTES);
-      so.store(nxt + NPAIR * QTile::BYTES);
-      if (threadIdx.x < BMQ) ((int TNPA_LDS*)(nxt + DSOFF))[threadIdx.x] = dsv;
+      for (int pr = 0; pr < NPAIR; ++pr) sq[pr].store(b1 + pr * QTile::BYTES);
+      so.store(b1 + NPAIR * QTile::BYTES);
+      if (threadIdx.x < BMQ) ((int TNPA_LDS*)(b1 + DSOFF))[threadIdx.x] = dsv;
     }
     __syncthreads();
-    cur ^= 1;
+    cur = next_buf(cur);
   };
   // Query tiles qlo, qlo+BMQ, ... < qhi, split per wave into: the diagonal (generic), tiles whose every query sees
   // every key of the wave (fast), and tiles past the wave's document end or the sequence end (generic).
@@ -987,33 +1145,56 @@ k_bwd_kv(const KParams p) {
   for (; j < j1; ++j) step(qlo + j * BMQ, std::true_type{});
   for (; j < ntile; ++j) step(qlo + j * BMQ, std::false_type{});
 
+  // dV and dK rows: scaled in registers, then (ROWLDS) gathered in LDS and written as whole rows
   const TDesc* kouts[2] = {&p.dk1, &p.dk2};
+  if constexpr (ROWLDS) {
+    if constexpr (WANT_DV) {
+      __syncthreads();  // every wave is done with the tile buffers
 #pragma unroll
-  for (int s = 0; s < KW; ++s) {
-    const int key = ka[s] + l32;
-    if (key >= T_) continue;
-    T* vrow = head_ptr_w<T>(p.dv, b, hd) + (int64_t)key * p.dv.st;
+      for (int s = 0; s < KW; ++s) acc_rows_to_lds<T, VRows, NDV>(smem, 32 * (wave * KW + s), l32, h, dv[s], p.vf, DV);
+      __syncthreads();
+      Stage<T, BNK, DV, DVP, NT> os;
+      os.copy_out(smem, head_ptr_w<T>(p.dv, b, hd), p.dv.st, n0, T_ - n0);
+    }
+    if constexpr (WANT_DK) {
 #pragma unroll
-    for (int d = 0; d < (WANT_DV ? NDV : 0); ++d)
+      for (int pr = 0; pr < NPAIR; ++pr) {
+        __syncthreads();  // every wave is done with the tile buffers (or with the previous rows)
 #pragma unroll
-      for (int g = 0; g < 4; ++g) {
-        const int col = 32 * d + 8 * g + 4 * h;
-        if (col < DV)
-          store4<T>(vrow + col, dv[s][d][4 * g] * p.vf, dv[s][d][4 * g + 1] * p.vf, dv[s][d][4 * g + 2] * p.vf,
-                    dv[s][d][4 * g + 3] * p.vf);
+        for (int s = 0; s < KW; ++s) acc_rows_to_lds<T, KRows, NDK>(smem, 32 * (wave * KW + s), l32, h, dk[pr][s], p.gf, DK);
+        __syncthreads();
+        Stage<T, BNK, DK, DKP, NT> os;
+        os.copy_out(smem, head_ptr_w<T>(*kouts[pr], b, hd), kouts[pr]->st, n0, T_ - n0);
       }
+    }
+  } else {
 #pragma unroll
-    for (int pr = 0; pr < (WANT_DK ? NPAIR : 0); ++pr) {
-      T* krow = head_ptr_w<T>(*kouts[pr], b, hd) + (int64_t)key * kouts[pr]->st;
+    for (int s = 0; s < KW; ++s) {
+      const int key = ka[s] + l32;
+      if (key >= T_) continue;
+      T* vrow = head_ptr_w<T>(p.dv, b, hd) + (int64_t)key * p.dv.st;
 #pragma unroll
-      for (int d = 0; d < NDK; ++d)
+      for (int d = 0; d < (WANT_DV ? NDV : 0); ++d)
 #pragma unroll
         for (int g = 0; g < 4; ++g) {
           const int col = 32 * d + 8 * g + 4 * h;
-          if (col < DK)
-            store4<T>(krow + col, dk[pr][s][d][4 * g] * p.gf, dk[pr][s][d][4 * g + 1] * p.gf,
-                      dk[pr][s][d][4 * g + 2] * p.gf, dk[pr][s][d][4 * g + 3] * p.gf);
+          if (col < DV)
+            store4<T>(vrow + col, dv[s][d][4 * g] * p.vf, dv[s][d][4 * g + 1] * p.vf, dv[s][d][4 * g + 2] * p.vf,
+                      dv[s][d][4 * g + 3] * p.vf);
         }
+#pragma unroll
+      for (int pr = 0; pr < (WANT_DK ? NPAIR : 0); ++pr) {
+        T* krow = head_ptr_w<T>(*kouts[pr], b, hd) + (int64_t)key * kouts[pr]->st;
+#pragma unroll
+        for (int d = 0; d < NDK; ++d)
+#pragma unroll
+          for (int g = 0; g < 4; ++g) {
+            const int col = 32 * d + 8 * g + 4 * h;
+            if (col < DK)
+              store4<T>(krow + col, dk[pr][s][d][4 * g] * p.gf, dk[pr][s][d][4 * g + 1] * p.gf,
+                        dk[pr][s][d][4 * g + 2] * p.gf, dk[pr][s][d][4 * g + 3] * p.gf);
+          }
+      }
     }
   }
 
