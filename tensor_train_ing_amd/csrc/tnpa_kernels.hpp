@@ -487,7 +487,10 @@ k_fwd(const KParams p) {
   auto step = [&](const int n0) {
     const int n1 = n0 + BN;
     const bool more = n1 < hi;
-    if (more) stage_load(n1);
+    if (more) {
+      if constexpr (CHUNKED) stage_load_buf(n1, 3);
+      else stage_load(n1);
+    }
     const char TNPA_LDS* base = smem + cur * BUF;
 #pragma unroll
     for (int kb = 0; kb < NKB; ++kb) {
@@ -503,7 +506,10 @@ k_fwd(const KParams p) {
       if (am == 0) continue;
       sub(base, n0, kb, am, fm, std::false_type{}, std::false_type{});
     }
-    if (more) stage_store(smem + next_buf(cur) * BUF, n1);
+    if (more) {
+      if constexpr (CHUNKED) stage_store_raw(smem + next_buf(cur) * BUF, 3);
+      else stage_store(smem + next_buf(cur) * BUF, n1);
+    }
     __syncthreads();
     cur = next_buf(cur);
   };
