@@ -193,6 +193,15 @@ k_fwd(const KParams p) {
         for (int c = 0; c < NCK; ++c) qf[pr][s][c] = valid ? load_op<T>(qp[pr] + (int64_t)q * qst[pr], c, h) : M::zero();
     }
   }
+  // the first K/V tile is loaded together with the Q rows (independent latencies); it is written to LDS once the
+  // Q fragments have been taken out of the same space
+  const int lo = (dst[m0] / BN) * BN;
+  const int hi = min(m0 + BM, T_);
+  Stage<T, BN, DK, DKP, NT> sk[NPAIR];
+  Stage<T, BN, DV, DVP, NT> sv;
+#pragma unroll
+  for (int pr = 0; pr < NPAIR; ++pr) sk[pr].load(kp[pr], kst[pr], lo, T_ - lo);
+  sv.load(vp, p.v.st, lo, T_ - lo);
   if constexpr (ROWLDS) {
     Stage<T, BM, DK, DKP, NT> qs[NPAIR];
 #pragma unroll
@@ -216,13 +225,6 @@ k_fwd(const KParams p) {
 #pragma unroll
     for (int d = 0; d < NDV; ++d) oacc[s][d] = zero16();
 
-  const int lo = (dst[m0] / BN) * BN;
-  const int hi = min(m0 + BM, T_);
-  Stage<T, BN, DK, DKP, NT> sk[NPAIR];
-  Stage<T, BN, DV, DVP, NT> sv;
-#pragma unroll
-  for (int pr = 0; pr < NPAIR; ++pr) sk[pr].load(kp[pr], kst[pr], lo, T_ - lo);
-  sv.load(vp, p.v.st, lo, T_ - lo);
 #pragma unroll
   for (int pr = 0; pr < NPAIR; ++pr) sk[pr].store(smem + pr * KTile::BYTES);
   sv.store(smem + NPAIR * KTile::BYTES);
