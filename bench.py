@@ -63,8 +63,8 @@ def time_events(fn, reps):
 
 
 def kernel_times(q, k, v, do, doc, rs, degree, reps):
-    """Average duration (ms) of each launch of the fwd, dK/dV and dQ kernels, timed with HIP events on the stream
-    the library launches on (torch's current stream)."""
+    """Average duration (ms) of each launch of the fwd, dV, dK and dQ kernels (and of the dO pre-scaling pass when the
+    operator uses it), timed with HIP events on the stream the library launches on (torch's current stream)."""
     import torch
     from tensor_train_ing_amd import _abi
     from tensor_train_ing_amd.poly_attn import _desc, _problem, _stream, doc_bounds
@@ -73,17 +73,20 @@ def kernel_times(q, k, v, do, doc, rs, degree, reps):
     prob = _problem(_abi.POWER, degree, q, k, q, k, v, dstart, qend, rs, None, None)
     o = torch.empty_like(v)
     dq, dk, dv = torch.empty_like(q), torch.empty_like(k), torch.empty_like(v)
-    dos = torch.empty_like(do)  # row-scaled dO workspace, as the operator passes it
-    grads = _abi.Grads(_desc(do), _desc(dq), _desc(dk), _desc(dq), _desc(dk), _desc(dv), None, None, _desc(dos))
+    # the row-scaled dO workspace, passed exactly when the operator passes it
+    dos = torch.empty_like(do) if lib.tnpa_dout_scaled_helps(ctypes.byref(prob)) else None
+    grads = _abi.Grads(_desc(do), _desc(dq), _desc(dk), _desc(dq), _desc(dk), _desc(dv), None, None,
+                       _desc(dos) if dos is not None else _abi.Tensor())
     st = _stream(q.device)
     od = _desc(o)
     def phase(ph, name):
         return lambda: _abi.check(lib.tnpa_backward_phase(ctypes.byref(prob), ctypes.byref(grads), ph, st), name)
     fwd = lambda: _abi.check(lib.tnpa_forward(ctypes.byref(prob), ctypes.byref(od), st), "fwd")  # noqa: E731
     out = {}
-    for name, fn in (("fwd", fwd), ("bwd_scale", phase(_abi.PHASE_KV_SCALE, "scale")),
-                     ("bwd_dv", phase(_abi.PHASE_KV_DV, "dv")), ("bwd_dk", phase(_abi.PHASE_KV_DK, "dk")),
-                     ("bwd_q", phase(_abi.PHASE_Q, "q"))):
+    runs = [("fwd", fwd)] + ([("bwd_scale", phase(_abi.PHASE_KV_SCALE, "scale"))] if dos is not None else []) + [
+        ("bwd_dv", phase(_abi.PHASE_KV_DV, "dv")), ("bwd_dk", phase(_abi.PHASE_KV_DK, "dk")),
+        ("bwd_q", phase(_abi.PHASE_Q, "q"))]
+    for name, fn in runs:
         for _ in range(3):
             fn()
         torch.cuda.synchronize()
@@ -191,7 +194,7 @@ def main(argv=None):
 
     kt = kernel_times(q.detach(), k.detach(), v.detach(), do, doc, rs, degree, a.kernel_reps)
     # matmul units of 2*B*H*Npairs*D each kernel executes: fwd QK^T + PV; dV pass S + dV; dK pass S + dP + dK;
-    # dQ pass S + dP + dQ (the row-scaling pass is a bandwidth kernel with no matrix work)
+    # dQ pass S + dP + dQ (the row-scaling pass, when used, is a bandwidth kernel with no matrix work)
     units = {"fwd": 2, "bwd_dv": 2, "bwd_dk": 3, "bwd_q": 3}
     dom = max(units, key=lambda n: kt[n])
     ach = units[dom] * 2.0 * B * H * npairs(T) * D / (kt[dom] * 1e-3) / 1e12

@@ -98,6 +98,11 @@ int tnpa_forward(const tnpa_problem_t* problem, const tnpa_tensor_t* out, void* 
 /* Floats of dpar_partial workspace tnpa_backward needs for this problem (0 for signed_product / power). */
 int64_t tnpa_dpar_workspace_floats(const tnpa_problem_t* problem);
 
+/* 1 if passing tnpa_grads_t.dout_scaled makes tnpa_backward faster for this problem, 0 if the dK/dV passes scale
+ * dout as cheaply themselves (16-bit inputs, one q/k pair, head dims multiples of 64) or the problem is NULL. No
+ * counterpart in the reference (a sizing query like tnpa_dpar_workspace_floats). */
+int32_t tnpa_dout_scaled_helps(const tnpa_problem_t* problem);
+
 /* Backward: writes dq1, dk1, (dq2, dk2), dv, and dpar. Replaces ref: tnlm/kernels/poly_attn.py:286-309
  * (PolyAttention.backward: _bwd_kv, _bwd_q and the fixed-order dcoef/db reduction). Deterministic: no atomics,
  * every reduction in a fixed order. */

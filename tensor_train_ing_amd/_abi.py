@@ -47,6 +47,7 @@ _SIGNATURES = {
                                        ctypes.c_int32, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p]),
     "tnpa_forward": (ctypes.c_int, [ctypes.POINTER(Problem), ctypes.POINTER(Tensor), ctypes.c_void_p]),
     "tnpa_dpar_workspace_floats": (ctypes.c_int64, [ctypes.POINTER(Problem)]),
+    "tnpa_dout_scaled_helps": (ctypes.c_int32, [ctypes.POINTER(Problem)]),
     "tnpa_backward": (ctypes.c_int, [ctypes.POINTER(Problem), ctypes.POINTER(Grads), ctypes.c_void_p]),
     "tnpa_backward_phase": (ctypes.c_int, [ctypes.POINTER(Problem), ctypes.POINTER(Grads), ctypes.c_int32,
                                            ctypes.c_void_p]),

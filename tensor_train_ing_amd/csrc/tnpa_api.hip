@@ -295,6 +295,12 @@ int64_t tnpa_dpar_workspace_floats(const tnpa_problem_t* problem) {
   return (int64_t)problem->batch * problem->heads * nnb * 4;
 }
 
+int32_t tnpa_dout_scaled_helps(const tnpa_problem_t* problem) {
+  if (problem == nullptr) return 0;
+  return tnpa::kv_scales_in_pass(problem->dtype == TNPA_F32, poly_of(*problem), problem->head_dim_k,
+                                 problem->head_dim_v) ? 0 : 1;
+}
+
 int tnpa_backward_phase(const tnpa_problem_t* problem, const tnpa_grads_t* grads, int32_t phases, void* stream) {
   int rc = check_problem(problem);
   if (rc) return rc;

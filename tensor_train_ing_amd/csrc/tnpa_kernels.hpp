@@ -853,6 +853,7 @@ k_bwd_kv(const KParams p) {
   // 160 KB of LDS and the tile splits evenly over the threads, else two (and for the two-pair kinds, whose single
   // key-side kernel is already short of registers)
   constexpr int NBUF = Stager::OK && NPAIR == 1 && NQB >= 2 && 3 * BUF <= 160 * 1024 ? 3 : 2;
+  static_assert((NBUF == 3) == kv_scales_in_pass(sizeof(T) == 4, POLY, DK, DV), "host mirror of the staging choice");
   // The block's K and V rows come in, and its dK / dV rows go out, through LDS as whole coalesced rows (ROWLDS;
   // not with zero-padded head dims, whose pad columns in the tile buffers must stay zero).
   typedef Tile<T, BNK, DKP> KRows;

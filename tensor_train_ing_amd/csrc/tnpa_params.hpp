@@ -43,6 +43,13 @@ inline bool kv_split(bool f32, int poly) { return !f32 && poly != POLY_GEN2; }
 // passes (two waves per SIMD), four for the one-wave-per-SIMD combined kernel.
 inline int kv_block_keys(bool f32, int poly) { return kv_split(f32, poly) ? 256 : 128; }
 
+// Whether the dK/dV passes scale dO by the row scale themselves at no cost: they stage the dO rows a step ahead and
+// apply the factor when writing them to LDS (three-buffer staging; 16-bit inputs, one q/k pair, head dims that
+// are multiples of 64). Then a separate pre-scaling pass costs more than it saves. Mirrors k_bwd_kv's NBUF == 3.
+constexpr bool kv_scales_in_pass(bool f32, int poly, int dk, int dv) {
+  return !f32 && poly != POLY_GEN2 && dk % 64 == 0 && dv % 64 == 0;
+}
+
 template <typename T, int POLY, int DK, int DV> hipError_t launch_fwd(const KParams& p, hipStream_t st);
 template <typename T, int POLY, int DK, int DV> hipError_t launch_bwd_kv(const KParams& p, hipStream_t st);
 template <typename T, int POLY, int DK, int DV> hipError_t launch_bwd_q(const KParams& p, hipStream_t st);

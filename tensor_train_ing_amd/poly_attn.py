@@ -164,11 +164,13 @@ class PolyAttention(torch.autograd.Function):
             ws = torch.empty(max(1, lib.tnpa_dpar_workspace_floats(ctypes.byref(prob))), dtype=torch.float32,
                              device=q1.device)
             dpar = torch.empty(H, 4, dtype=torch.float32, device=q1.device)
-        # row_scale * dO, written by the library before its dK/dV pass and streamed by it (one pass over dO
-        # instead of a rescale per key block)
-        dos = torch.empty(do.shape, dtype=do.dtype, device=do.device)
+        # row_scale * dO, written by the library before its dK/dV pass and streamed by it, where that beats the pass
+        # scaling dO itself
+        dos = (torch.empty(do.shape, dtype=do.dtype, device=do.device)
+               if lib.tnpa_dout_scaled_helps(ctypes.byref(prob)) else None)
         g = _abi.Grads(_desc(do), _desc(dq1), _desc(dk1), _desc(dq2), _desc(dk2), _desc(dv),
-                       ws.data_ptr() if par else None, dpar.data_ptr() if par else None, _desc(dos))
+                       ws.data_ptr() if par else None, dpar.data_ptr() if par else None,
+                       _desc(dos) if dos is not None else _abi.Tensor())
         with torch.cuda.device(q1.device):
             _abi.check(lib.tnpa_backward(ctypes.byref(prob), ctypes.byref(g), _stream(q1.device)),
                        "poly_attention backward")
