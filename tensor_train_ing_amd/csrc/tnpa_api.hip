@@ -155,47 +155,116 @@ hipError_t run(int ph, const tnpa_problem_t& p, const tnpa::KParams& k, hipStrea
 }
 
 // ---------------------------------------------------------------------------------------------- prepass kernels
-// One workgroup per batch row. doc_start[t] = start of t's run (t + 1 for padding) via a max-scan of run starts;
-// query_end[t] = next run start after t (t for padding) via a reverse min-scan.
-__global__ void __launch_bounds__(256) k_doc_bounds(const void* doc, int is64, int64_t sb, int T, int* dstart,
-                                                    int* qend) {
-  constexpr int NT = 256;
-  const int b = blockIdx.x, t = threadIdx.x;
-  const int L = (T + NT - 1) / NT;
-  const int s0 = min(t * L, T), s1 = min(s0 + L, T);
+// One workgroup of 1024 threads per batch row. A run start is a token whose id differs from its predecessor's;
+// doc_start[t] = last run start <= t (t + 1 for padding), query_end[t] = first run start > t, or T (t for padding).
+// The row goes through LDS in chunks of 4096 ids (coalesced loads; each thread then owns 4 consecutive tokens and
+// writes them as one 16-byte store): a forward pass carries the last start across chunks with a max-scan, a
+// backward pass the next start with a min-scan, starting on the chunk the forward pass left in LDS.
+__global__ void __launch_bounds__(1024) k_doc_bounds(const void* doc, int is64, int64_t sb, int T, int* dstart,
+                                                     int* qend) {
+  constexpr int NT = 1024, L = 4, CH = NT * L, NW = NT / 64;
+  __shared__ int64_t sid[CH + 1];  // sid[k] = id(c0 - 1 + k)
+  __shared__ int wred[NW];
+  const int b = blockIdx.x, t = threadIdx.x, lane = t & 63, w = t >> 6;
   const int64_t* d64 = (const int64_t*)doc + (int64_t)b * sb;
   const int* d32 = (const int*)doc + (int64_t)b * sb;
-  auto id = [&](int i) -> int64_t { return is64 ? d64[i] : (int64_t)d32[i]; };
-  auto is_start = [&](int i) -> bool { return i == 0 || id(i) != id(i - 1); };
-  int last = -1, first = T;
-  for (int i = s0; i < s1; ++i)
-    if (is_start(i)) {
-      last = i;
-      if (first == T) first = i;
-    }
-  __shared__ int sl[NT], sf[NT];
-  sl[t] = last;
-  sf[t] = first;
-  __syncthreads();
-  for (int off = 1; off < NT; off <<= 1) {
-    const int a = t >= off ? sl[t - off] : -1;
-    const int c = t + off < NT ? sf[t + off] : T;
-    __syncthreads();
-    sl[t] = max(sl[t], a);
-    sf[t] = min(sf[t], c);
-    __syncthreads();
-  }
-  int cur = t > 0 ? sl[t - 1] : -1;
-  int nxt = t < NT - 1 ? sf[t + 1] : T;
   int* ds = dstart + (int64_t)b * T;
   int* qe = qend + (int64_t)b * T;
-  for (int i = s0; i < s1; ++i) {
-    if (is_start(i)) cur = i;
-    ds[i] = id(i) < 0 ? i + 1 : cur;
+  auto load_chunk = [&](int c0, int n) {
+    for (int k = t; k <= n; k += NT) {
+      const int i = c0 - 1 + k;
+      sid[k] = i < 0 ? INT64_MIN : (is64 ? d64[i] : (int64_t)d32[i]);
+    }
+    __syncthreads();
+  };
+  // run start at chunk offset k (token c0 + k)
+  auto start_at = [&](int c0, int k) { return c0 + k == 0 || sid[k + 1] != sid[k]; };
+
+  int carry = -1;  // last run start before the chunk
+  for (int c0 = 0; c0 < T; c0 += CH) {
+    const int n = min(CH, T - c0);
+    load_chunk(c0, n);
+    int last = -1;
+#pragma unroll
+    for (int j = 0; j < L; ++j) {
+      const int k = t * L + j;
+      if (k < n && start_at(c0, k)) last = c0 + k;
+    }
+    int x = last;  // inclusive max-scan over the threads
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+      const int y = __shfl_up(x, o, 64);
+      if (lane >= o) x = max(x, y);
+    }
+    if (lane == 63) wred[w] = x;
+    __syncthreads();
+    int cur = carry, all = carry;
+    for (int v = 0; v < NW; ++v) {
+      if (v < w) cur = max(cur, wred[v]);
+      all = max(all, wred[v]);
+    }
+    const int prev = __shfl_up(x, 1, 64);
+    if (lane > 0) cur = max(cur, prev);
+    if (t * L < n) {
+      int o[L];
+#pragma unroll
+      for (int j = 0; j < L; ++j) {
+        const int k = t * L + j;
+        if (k < n && start_at(c0, k)) cur = c0 + k;
+        o[j] = k < n && sid[k + 1] < 0 ? c0 + k + 1 : cur;
+      }
+      if (c0 + t * L + L <= T && ((uintptr_t)(ds + c0 + t * L) & 15) == 0) {
+        *(int4*)(ds + c0 + t * L) = make_int4(o[0], o[1], o[2], o[3]);
+      } else {
+        for (int j = 0; j < L && t * L + j < n; ++j) ds[c0 + t * L + j] = o[j];
+      }
+    }
+    carry = all;
+    __syncthreads();  // before the next chunk overwrites sid and wred
   }
-  for (int i = s1 - 1; i >= s0; --i) {
-    qe[i] = id(i) < 0 ? i : nxt;
-    if (is_start(i)) nxt = i;
+
+  int carry2 = T;  // first run start after the chunk
+  const int clast = ((T - 1) / CH) * CH;  // still in LDS from the forward pass
+  for (int c0 = clast; c0 >= 0; c0 -= CH) {
+    const int n = min(CH, T - c0);
+    if (c0 != clast) load_chunk(c0, n);
+    int first = T;
+#pragma unroll
+    for (int j = L - 1; j >= 0; --j) {
+      const int k = t * L + j;
+      if (k < n && start_at(c0, k)) first = c0 + k;
+    }
+    int x = first;  // inclusive min-scan over the threads, from the end
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+      const int y = __shfl_down(x, o, 64);
+      if (lane + o < 64) x = min(x, y);
+    }
+    if (lane == 0) wred[w] = x;
+    __syncthreads();
+    int nxt = carry2, all = carry2;
+    for (int v = 0; v < NW; ++v) {
+      if (v > w) nxt = min(nxt, wred[v]);
+      all = min(all, wred[v]);
+    }
+    const int after = __shfl_down(x, 1, 64);
+    if (lane < 63) nxt = min(nxt, after);
+    if (t * L < n) {
+      int o[L];
+#pragma unroll
+      for (int j = L - 1; j >= 0; --j) {
+        const int k = t * L + j;
+        o[j] = k < n && sid[k + 1] < 0 ? c0 + k : nxt;
+        if (k < n && start_at(c0, k)) nxt = c0 + k;
+      }
+      if (c0 + t * L + L <= T && ((uintptr_t)(qe + c0 + t * L) & 15) == 0) {
+        *(int4*)(qe + c0 + t * L) = make_int4(o[0], o[1], o[2], o[3]);
+      } else {
+        for (int j = 0; j < L && t * L + j < n; ++j) qe[c0 + t * L + j] = o[j];
+      }
+    }
+    carry2 = all;
+    __syncthreads();
   }
 }
 
@@ -268,7 +337,7 @@ int tnpa_doc_bounds(const void* doc_ids, int32_t doc_is_int64, int64_t doc_strid
   if (batch <= 0 || seq_len <= 0) return fail(TNPA_ERR_INVALID, "tnpa_doc_bounds: batch and seq_len must be positive");
   if (batch > 1 && doc_stride_b < seq_len)
     return fail(TNPA_ERR_INVALID, "tnpa_doc_bounds: batch stride %lld shorter than seq_len", (long long)doc_stride_b);
-  hipLaunchKernelGGL(k_doc_bounds, dim3(batch), dim3(256), 0, (hipStream_t)stream, doc_ids, doc_is_int64 ? 1 : 0,
+  hipLaunchKernelGGL(k_doc_bounds, dim3(batch), dim3(1024), 0, (hipStream_t)stream, doc_ids, doc_is_int64 ? 1 : 0,
                      doc_stride_b, seq_len, doc_start, query_end);
   const hipError_t e = hipGetLastError();
   if (e != hipSuccess) return fail(TNPA_ERR_LAUNCH, "tnpa_doc_bounds: %s", hipGetErrorString(e));

@@ -358,3 +358,32 @@ def test_baseline_config_bf16_full_size(name):
     errs = compare(res, ref, ["out", "dq1", "dk1", "dv"])
     print(name, {n: f"fro={e[0]:.2e} max={e[1]:.2e}" for n, e in errs.items()}, flush=True)
     _check(errs, BF16_FRO, BF16_MAX)
+
+
+@pytest.mark.parametrize("T", [1, 3, 300, 4096, 4100, 5000])
+@pytest.mark.parametrize("dtype", [torch.int32, torch.int64])
+def test_doc_bounds_match_oracle(T, dtype):
+    """tnpa_doc_bounds (one workgroup per row, 4096-token LDS chunks) against the brute-force oracle: uneven
+    documents (contiguous runs of one id, as the operator requires), documents crossing a chunk edge, interior and
+    trailing padding, rows with a batch stride longer than T, int32 and int64 ids."""
+    import sys
+    sys.path.insert(0, str(Path(__file__).resolve().parents[1]))
+    from oracle import doc_bounds as oracle_bounds
+    from tensor_train_ing_amd.poly_attn import doc_bounds
+    g = torch.Generator().manual_seed(T)
+    B = 3
+    wide = torch.full((B, T + 5), 99, dtype=torch.long)
+    for bi in range(B):
+        cuts = sorted(set(torch.randint(0, T, (1 + bi * 3,), generator=g).tolist() + [0, min(T - 1, 4095)]))
+        for i, st in enumerate(cuts):
+            wide[bi, st:T] = i
+    if T > 8:
+        # interior padding; the ids after it are new documents (ids are contiguous runs, the operator's contract)
+        wide[1, T // 3 + 5:T] += 1000
+        wide[1, T // 3:T // 3 + 5] = -1
+        wide[2, T - T // 4:T] = -1  # trailing padding
+    doc = wide.to(dtype)[:, :T]  # batch stride T + 5
+    ds, qe = doc_bounds(doc.cuda())
+    rs, rq = oracle_bounds(wide[:, :T].numpy())
+    np.testing.assert_array_equal(ds.cpu().numpy(), rs)
+    np.testing.assert_array_equal(qe.cpu().numpy(), rq)
