@@ -246,21 +246,6 @@ template <typename T, int ROWS, int D, int WID, int NT> struct Stage {
     const int idx = (int)threadIdx.x + i * NT;
     *(u32x4 TNPA_LDS*)(tile + TL::off(idx / NCHG, (idx % NCHG) * CE)) = r[i];
   }
-  // Branch-free form of load() for one chunk, so it can be scheduled between matrix instructions: the row is clamped
-  // to rmax (a valid row) instead of skipped; store_chunk() zeroes rows at or beyond nvalid. Needs TOTAL % NT == 0.
-  __device__ inline void load_chunk(int i, const T* __restrict__ g, int64_t st, int row0, int rmax) {
-    static_assert(TOTAL % NT == 0, "every thread owns PER chunks");
-    const int idx = (int)threadIdx.x + i * NT;
-    const int rr = idx / NCHG, c = idx % NCHG;
-    r[i] = *(const u32x4*)(g + (int64_t)min(row0 + rr, rmax) * st + c * CE);
-  }
-  __device__ inline void store_chunk(int i, char TNPA_LDS* tile, int nvalid) const {
-    const int idx = (int)threadIdx.x + i * NT;
-    const int rr = idx / NCHG, c = idx % NCHG;
-    const bool ok = rr < nvalid;
-    *(u32x4 TNPA_LDS*)(tile + TL::off(rr, c * CE)) =
-        u32x4{ok ? r[i][0] : 0u, ok ? r[i][1] : 0u, ok ? r[i][2] : 0u, ok ? r[i][3] : 0u};
-  }
 };
 
 // Buffer resource over rows n1.. of one (b, h) head of row stride st (elements) and D real columns: rows at or

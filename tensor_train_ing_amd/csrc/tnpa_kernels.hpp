@@ -283,36 +283,6 @@ k_fwd(const KParams p) {
   typedef Stage<T, BN, DK, DKP, NT> KStage;
   typedef Stage<T, BN, DV, DVP, NT> VStage;
   auto next_buf = [](const int c) { return c + 1 == NBUF ? 0 : c + 1; };
-  // Global -> register staging of the tile at rows n1.. and its store into an LDS buffer. The chunked form is
-  // branch-free (clamped rows, zeroed in the store), so it can sit between matrix instructions.
-  auto stage_load = [&](const int n1) {
-    if constexpr (CHUNKED) {
-#pragma unroll
-      for (int pr = 0; pr < NPAIR; ++pr)
-#pragma unroll
-        for (int i = 0; i < KStage::PER; ++i) sk[pr].load_chunk(i, kp[pr], kst[pr], n1, T_ - 1);
-#pragma unroll
-      for (int i = 0; i < VStage::PER; ++i) sv.load_chunk(i, vp, p.v.st, n1, T_ - 1);
-    } else {
-#pragma unroll
-      for (int pr = 0; pr < NPAIR; ++pr) sk[pr].load(kp[pr], kst[pr], n1, T_ - n1);
-      sv.load(vp, p.v.st, n1, T_ - n1);
-    }
-  };
-  auto stage_store = [&](char TNPA_LDS* dstb, const int n1) {
-    if constexpr (CHUNKED) {
-#pragma unroll
-      for (int pr = 0; pr < NPAIR; ++pr)
-#pragma unroll
-        for (int i = 0; i < KStage::PER; ++i) sk[pr].store_chunk(i, dstb + pr * KTile::BYTES, T_ - n1);
-#pragma unroll
-      for (int i = 0; i < VStage::PER; ++i) sv.store_chunk(i, dstb + NPAIR * KTile::BYTES, T_ - n1);
-    } else {
-#pragma unroll
-      for (int pr = 0; pr < NPAIR; ++pr) sk[pr].store(dstb + pr * KTile::BYTES);
-      sv.store(dstb + NPAIR * KTile::BYTES);
-    }
-  };
   auto k_rows = [&](Op (&ka)[NPAIR][NCK], const char TNPA_LDS* base, const int kb) {
 #pragma unroll
     for (int pr = 0; pr < NPAIR; ++pr)
@@ -399,6 +369,26 @@ k_fwd(const KParams p) {
       for (int i = 0; i < VStage::PER; ++i) sv.store_raw(i, dstb + NPAIR * KTile::BYTES);
     }
   };
+  // Whole-tile staging of rows n1.. (buffer loads when the tile splits evenly over the threads, else the guarded
+  // per-chunk copy)
+  auto stage_load = [&](const int n1) {
+    if constexpr (CHUNKED) {
+      stage_load_buf(n1, 3);
+    } else {
+#pragma unroll
+      for (int pr = 0; pr < NPAIR; ++pr) sk[pr].load(kp[pr], kst[pr], n1, T_ - n1);
+      sv.load(vp, p.v.st, n1, T_ - n1);
+    }
+  };
+  auto stage_store = [&](char TNPA_LDS* dstb) {
+    if constexpr (CHUNKED) {
+      stage_store_raw(dstb, 3);
+    } else {
+#pragma unroll
+      for (int pr = 0; pr < NPAIR; ++pr) sk[pr].store(dstb + pr * KTile::BYTES);
+      sv.store(dstb + NPAIR * KTile::BYTES);
+    }
+  };
 
   // Run of unmasked tiles jb..je-1 (no mask, no sub-block test).
   // Three buffers: software pipeline over the run's 32-key sub-blocks g. Phase A(g): the V^T(g) reads and the
@@ -477,7 +467,7 @@ k_fwd(const KParams p) {
           power(pop, sacc);
           pv_mma(vt, pop);
         }
-        if (more) stage_store(smem + next_buf(cur) * BUF, n1);
+        if (more) stage_store(smem + next_buf(cur) * BUF);
         __syncthreads();
         cur = next_buf(cur);
       }
@@ -489,10 +479,7 @@ k_fwd(const KParams p) {
   auto step = [&](const int n0) {
     const int n1 = n0 + BN;
     const bool more = n1 < hi;
-    if (more) {
-      if constexpr (CHUNKED) stage_load_buf(n1, 3);
-      else stage_load(n1);
-    }
+    if (more) stage_load(n1);
     const char TNPA_LDS* base = smem + cur * BUF;
 #pragma unroll
     for (int kb = 0; kb < NKB; ++kb) {
@@ -508,10 +495,7 @@ k_fwd(const KParams p) {
       if (am == 0) continue;
       sub(base, n0, kb, am, fm, std::false_type{}, std::false_type{});
     }
-    if (more) {
-      if constexpr (CHUNKED) stage_store_raw(smem + next_buf(cur) * BUF, 3);
-      else stage_store(smem + next_buf(cur) * BUF, n1);
-    }
+    if (more) stage_store(smem + next_buf(cur) * BUF);
     __syncthreads();
     cur = next_buf(cur);
   };
