@@ -19,4 +19,6 @@ namespace tnpa {
 TNPA_INST_DVS(POLY_GEN1)
 TNPA_INST_DVS(POLY_GEN2)
 TNPA_INST_DVS(POLY_POW2)
+TNPA_INST_DVS(POLY_POW4)
+TNPA_INST_DVS(POLY_OS)
 }  // namespace tnpa

@@ -43,19 +43,28 @@ __device__ inline Coefs load_coefs(const KParams& p, int hd) {
   return c;
 }
 
+// x^e for a wave-uniform exponent 0 <= e <= 15, by squaring: the exponent bits select factors (no loop, no branch).
+__device__ inline float upow(float x, int e) {
+  const float x2 = x * x, x4 = x2 * x2;
+  float v = (e & 1) ? x : 1.0f;
+  v = (e & 2) ? v * x2 : v;
+  v = (e & 4) ? v * x4 : v;
+  return (e & 8) ? v * (x4 * x4) : v;
+}
+
 // A(S1, S2) on raw dot products r = q.k (homogeneous kinds fold sm^p into vf).  ref: tnlm/kernels/poly_attn.py:26-34
 template <int POLY>
 __device__ inline float poly_value(float r1, float r2, int kind, int deg, float sm, const Coefs& c) {
   if constexpr (POLY == POLY_POW2) {
     return r1 * r1;
+  } else if constexpr (POLY == POLY_POW4) {
+    const float a2 = r1 * r1;
+    return a2 * a2;
+  } else if constexpr (POLY == POLY_OS) {
+    const float t = fmaf(r1, sm, c.c0);
+    return t * t;
   } else if constexpr (POLY == POLY_GEN1) {
-    if (kind == KIND_OS) {
-      const float t = fmaf(r1, sm, c.c0);
-      return t * t;
-    }
-    float v = r1;
-    for (int i = 1; i < deg; ++i) v *= r1;
-    return v;
+    return upow(r1, deg);
   } else {
     if (kind == KIND_SP) return r1 * r2;
     const float s1 = r1 * sm, s2 = r2 * sm;
@@ -71,16 +80,16 @@ __device__ inline void poly_grad(float r1, float r2, float hg, int kind, int deg
   if constexpr (POLY == POLY_POW2) {
     d1 = hg * r1;
     d2 = 0.f;
-  } else if constexpr (POLY == POLY_GEN1) {
+  } else if constexpr (POLY == POLY_POW4) {
+    d1 = hg * (r1 * (r1 * r1));
     d2 = 0.f;
-    if (kind == KIND_OS) {
-      d1 = 2.0f * hg * fmaf(r1, sm, c.c0);
-      if constexpr (PAR) g[0] += d1;
-    } else {
-      float v = 1.0f;
-      for (int i = 1; i < deg; ++i) v *= r1;
-      d1 = hg * v;
-    }
+  } else if constexpr (POLY == POLY_OS) {
+    d1 = 2.0f * hg * fmaf(r1, sm, c.c0);
+    d2 = 0.f;
+    if constexpr (PAR) g[0] += d1;
+  } else if constexpr (POLY == POLY_GEN1) {
+    d1 = hg * upow(r1, deg - 1);
+    d2 = 0.f;
   } else {
     if (kind == KIND_SP) {
       d1 = hg * r2;
@@ -824,7 +833,7 @@ k_bwd_kv(const KParams p) {
   typedef typename M::Op Op;
   constexpr int KC = M::KC, EPL = M::EPL, NT = NW * 64;
   constexpr int NPAIR = POLY == POLY_GEN2 ? 2 : 1;
-  constexpr bool PAR = POLY != POLY_POW2 && MODE != KV_DV;
+  constexpr bool PAR = (POLY == POLY_OS || POLY == POLY_GEN2) && MODE != KV_DV;  // kinds with head scalars
   constexpr bool WANT_DV = MODE != KV_DK, WANT_DK = MODE != KV_DV;
   constexpr int DKP = DK < 32 ? 32 : DK, DVP = DV < 32 ? 32 : DV;
   constexpr int NCK = DK / KC, NCV = DV / KC, NDK = DKP / 32, NDV = DVP / 32, NQB = BMQ / 32, NC2 = 32 / KC;

@@ -8,9 +8,10 @@
 namespace tnpa {
 
 enum Kind { KIND_SP = 0, KIND_OS = 1, KIND_LDM = 2, KIND_POW = 3 };
-// Compile-time polynomial families: GEN1 = one q/k pair (offset_square, power of any degree), GEN2 = two pairs
-// (signed_product, lower_degree_mix), POW2 = power of degree 2 (also signed_product with shared pairs).
-enum Poly { POLY_GEN1 = 0, POLY_GEN2 = 1, POLY_POW2 = 2 };
+// Compile-time polynomial families, so that no kind or degree test sits in the inner loops: GEN1 = power of another
+// degree (1, 3, 5..8; exponent bits applied with selects), GEN2 = two pairs (signed_product, lower_degree_mix),
+// POW2 / POW4 = power of degree 2 (also signed_product with shared pairs) / 4, OS = offset_square.
+enum Poly { POLY_GEN1 = 0, POLY_GEN2 = 1, POLY_POW2 = 2, POLY_POW4 = 3, POLY_OS = 4 };
 
 struct TDesc {
   const void* p;
