@@ -117,7 +117,7 @@ tnpa::KParams make_params(const tnpa_problem_t& p) {
 int poly_of(const tnpa_problem_t& p) {
   if (p.kind == TNPA_POWER) return p.degree == 2 ? tnpa::POLY_POW2 : p.degree == 4 ? tnpa::POLY_POW4 : tnpa::POLY_GEN1;
   if (p.kind == TNPA_OFFSET_SQUARE) return tnpa::POLY_OS;
-  return tnpa::POLY_GEN2;
+  return p.kind == TNPA_SIGNED_PRODUCT ? tnpa::POLY_SP : tnpa::POLY_GEN2;
 }
 
 enum Phase { PH_FWD = 0, PH_BWD_KV = 1, PH_BWD_Q = 2 };
@@ -143,6 +143,7 @@ hipError_t run_poly(int ph, int poly, int dk, int dv, const tnpa::KParams& k, hi
     case tnpa::POLY_GEN2: return run_dims<T, tnpa::POLY_GEN2>(ph, dk, dv, k, s);
     case tnpa::POLY_POW4: return run_dims<T, tnpa::POLY_POW4>(ph, dk, dv, k, s);
     case tnpa::POLY_OS: return run_dims<T, tnpa::POLY_OS>(ph, dk, dv, k, s);
+    case tnpa::POLY_SP: return run_dims<T, tnpa::POLY_SP>(ph, dk, dv, k, s);
     default: return run_dims<T, tnpa::POLY_POW2>(ph, dk, dv, k, s);
   }
 }

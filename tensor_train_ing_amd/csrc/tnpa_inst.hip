@@ -21,4 +21,5 @@ TNPA_INST_DVS(POLY_GEN2)
 TNPA_INST_DVS(POLY_POW2)
 TNPA_INST_DVS(POLY_POW4)
 TNPA_INST_DVS(POLY_OS)
+TNPA_INST_DVS(POLY_SP)
 }  // namespace tnpa

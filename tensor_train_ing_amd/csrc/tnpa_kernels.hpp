@@ -53,7 +53,9 @@ __device__ inline float upow(float x, int e) {
 }
 
 // A(S1, S2) on raw dot products r = q.k (homogeneous kinds fold sm^p into vf).  ref: tnlm/kernels/poly_attn.py:26-34
-template <int POLY>
+// KINDTEST (two-pair families only) keeps a never-taken test of the kind in the lower_degree_mix code: it changes
+// nothing in the results, but without it the one-wave dK/dV kernel of that kind needs 4x more scratch spills.
+template <int POLY, bool KINDTEST = false>
 __device__ inline float poly_value(float r1, float r2, int kind, int deg, float sm, const Coefs& c) {
   if constexpr (POLY == POLY_POW2) {
     return r1 * r1;
@@ -65,8 +67,10 @@ __device__ inline float poly_value(float r1, float r2, int kind, int deg, float 
     return t * t;
   } else if constexpr (POLY == POLY_GEN1) {
     return upow(r1, deg);
+  } else if constexpr (POLY == POLY_SP) {
+    return r1 * r2;
   } else {
-    if (kind == KIND_SP) return r1 * r2;
+    if (KINDTEST && kind == KIND_SP) return r1 * r2;
     const float s1 = r1 * sm, s2 = r2 * sm;
     return c.c0 + c.c1 * s1 + c.c2 * s2 + c.c12 * s1 * s2;
   }
@@ -74,7 +78,7 @@ __device__ inline float poly_value(float r1, float r2, int kind, int deg, float 
 
 // dS1, dS2 for a masked upstream H entry hg (gf carries the constant factors); optionally accumulates the
 // head-scalar partial sums g[0..3].  ref: tnlm/kernels/poly_attn.py:123-135,189-196
-template <int POLY, bool PAR>
+template <int POLY, bool PAR, bool KINDTEST = false>
 __device__ inline void poly_grad(float r1, float r2, float hg, int kind, int deg, float sm, const Coefs& c,
                                  float& d1, float& d2, float* g) {
   if constexpr (POLY == POLY_POW2) {
@@ -90,8 +94,11 @@ __device__ inline void poly_grad(float r1, float r2, float hg, int kind, int deg
   } else if constexpr (POLY == POLY_GEN1) {
     d1 = hg * upow(r1, deg - 1);
     d2 = 0.f;
+  } else if constexpr (POLY == POLY_SP) {
+    d1 = hg * r2;
+    d2 = hg * r1;
   } else {
-    if (kind == KIND_SP) {
+    if (KINDTEST && kind == KIND_SP) {
       d1 = hg * r2;
       d2 = hg * r1;
     } else {
@@ -123,7 +130,7 @@ __host__ __device__ constexpr int cmax(int a, int b) { return a > b ? a : b; }
 // register allocation must allow (2 lets a second wave hide the first one's LDS latency).
 template <typename T, int POLY, int DK, int DV> struct Cfg {
   static constexpr bool F32 = sizeof(T) == 4;
-  static constexpr int NPAIR = POLY == POLY_GEN2 ? 2 : 1;
+  static constexpr int NPAIR = two_pair_poly(POLY) ? 2 : 1;
   // two waves per SIMD (16-bit, one pair): eight waves per workgroup, so each staged tile serves 256 rows
   static constexpr bool TWO = !F32 && NPAIR == 1;
   static constexpr int FW_NW = TWO ? 8 : 4, FW_QW = 1, FW_BN = F32 ? 32 : 64, FW_WPE = TWO ? 2 : 1;
@@ -141,7 +148,7 @@ k_fwd(const KParams p) {
   typedef Mfma<T> M;
   typedef typename M::Op Op;
   constexpr int KC = M::KC, EPL = M::EPL, NT = NW * 64;
-  constexpr int NPAIR = POLY == POLY_GEN2 ? 2 : 1;
+  constexpr int NPAIR = two_pair_poly(POLY) ? 2 : 1;
   constexpr int DKP = DK < 32 ? 32 : DK, DVP = DV < 32 ? 32 : DV;
   constexpr int NCK = DK / KC, NDV = DVP / 32, NKB = BN / 32, NC2 = 32 / KC;
   constexpr int BM = NW * QW * 32;
@@ -543,7 +550,7 @@ k_bwd_q(const KParams p) {
   typedef Mfma<T> M;
   typedef typename M::Op Op;
   constexpr int KC = M::KC, EPL = M::EPL, NT = NW * 64;
-  constexpr int NPAIR = POLY == POLY_GEN2 ? 2 : 1;
+  constexpr int NPAIR = two_pair_poly(POLY) ? 2 : 1;
   constexpr int DKP = DK < 32 ? 32 : DK, DVP = DV < 32 ? 32 : DV;
   constexpr int NCK = DK / KC, NCV = DV / KC, NDK = DKP / 32, NKB = BN / 32, NC2 = 32 / KC;
   constexpr int BM = NW * QW * 32;
@@ -832,7 +839,7 @@ k_bwd_kv(const KParams p) {
   typedef Mfma<T> M;
   typedef typename M::Op Op;
   constexpr int KC = M::KC, EPL = M::EPL, NT = NW * 64;
-  constexpr int NPAIR = POLY == POLY_GEN2 ? 2 : 1;
+  constexpr int NPAIR = two_pair_poly(POLY) ? 2 : 1;
   constexpr bool PAR = (POLY == POLY_OS || POLY == POLY_GEN2) && MODE != KV_DV;  // kinds with head scalars
   constexpr bool WANT_DV = MODE != KV_DK, WANT_DK = MODE != KV_DV;
   constexpr int DKP = DK < 32 ? 32 : DK, DVP = DV < 32 ? 32 : DV;
@@ -1013,8 +1020,8 @@ k_bwd_kv(const KParams p) {
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
           const float r1 = sacc[0][s][r], r2 = sacc[NPAIR - 1][s][r];
-          if constexpr (WANT_DV) pv[r] = poly_value<POLY>(r1, r2, p.kind, p.deg, p.sm, cf);
-          if constexpr (WANT_DK) poly_grad<POLY, PAR>(r1, r2, pacc[s][r], p.kind, p.deg, p.sm, cf, d1[r], d2[r], gsum);
+          if constexpr (WANT_DV) pv[r] = poly_value<POLY, MODE == KV_BOTH>(r1, r2, p.kind, p.deg, p.sm, cf);
+          if constexpr (WANT_DK) poly_grad<POLY, PAR, MODE == KV_BOTH>(r1, r2, pacc[s][r], p.kind, p.deg, p.sm, cf, d1[r], d2[r], gsum);
         }
       } else {
         const int key = ka[s] + l32;
@@ -1023,9 +1030,9 @@ k_bwd_kv(const KParams p) {
           const int qo = 32 * qb + key_off<T>(r, h);
           const bool vis = key <= m + qo && dsl[qo] <= key;
           const float r1 = sacc[0][s][r], r2 = sacc[NPAIR - 1][s][r];
-          if constexpr (WANT_DV) pv[r] = vis ? poly_value<POLY>(r1, r2, p.kind, p.deg, p.sm, cf) : 0.f;
+          if constexpr (WANT_DV) pv[r] = vis ? poly_value<POLY, MODE == KV_BOTH>(r1, r2, p.kind, p.deg, p.sm, cf) : 0.f;
           if constexpr (WANT_DK)
-            poly_grad<POLY, PAR>(r1, r2, vis ? pacc[s][r] : 0.f, p.kind, p.deg, p.sm, cf, d1[r], d2[r], gsum);
+            poly_grad<POLY, PAR, MODE == KV_BOTH>(r1, r2, vis ? pacc[s][r] : 0.f, p.kind, p.deg, p.sm, cf, d1[r], d2[r], gsum);
         }
       }
 #pragma unroll

@@ -9,9 +9,11 @@ namespace tnpa {
 
 enum Kind { KIND_SP = 0, KIND_OS = 1, KIND_LDM = 2, KIND_POW = 3 };
 // Compile-time polynomial families, so that no kind or degree test sits in the inner loops: GEN1 = power of another
-// degree (1, 3, 5..8; exponent bits applied with selects), GEN2 = two pairs (signed_product, lower_degree_mix),
-// POW2 / POW4 = power of degree 2 (also signed_product with shared pairs) / 4, OS = offset_square.
-enum Poly { POLY_GEN1 = 0, POLY_GEN2 = 1, POLY_POW2 = 2, POLY_POW4 = 3, POLY_OS = 4 };
+// degree (1, 3, 5..8; exponent bits applied with selects), GEN2 = lower_degree_mix, SP = signed_product with two
+// distinct pairs, POW2 / POW4 = power of degree 2 (also signed_product with shared pairs) / 4, OS = offset_square.
+enum Poly { POLY_GEN1 = 0, POLY_GEN2 = 1, POLY_POW2 = 2, POLY_POW4 = 3, POLY_OS = 4, POLY_SP = 5 };
+// The families with two q/k pairs (two score products per key).
+constexpr bool two_pair_poly(int poly) { return poly == POLY_GEN2 || poly == POLY_SP; }
 
 struct TDesc {
   const void* p;
@@ -38,7 +40,7 @@ struct KParams {
 };
 
 // Whether the key side runs as separate dV and dK passes (16-bit inputs, one q/k pair); mirrors Cfg::KV_SPLIT.
-inline bool kv_split(bool f32, int poly) { return !f32 && poly != POLY_GEN2; }
+inline bool kv_split(bool f32, int poly) { return !f32 && !two_pair_poly(poly); }
 
 // Keys per dK/dV workgroup (sizes the dcoef/db partials); mirrors Cfg::KV_KEYS: eight waves of 32 keys for the split
 // passes (two waves per SIMD), four for the one-wave-per-SIMD combined kernel.
@@ -48,7 +50,7 @@ inline int kv_block_keys(bool f32, int poly) { return kv_split(f32, poly) ? 256 
 // apply the factor when writing them to LDS (three-buffer staging; 16-bit inputs, one q/k pair, head dims that
 // are multiples of 64). Then a separate pre-scaling pass costs more than it saves. Mirrors k_bwd_kv's NBUF == 3.
 constexpr bool kv_scales_in_pass(bool f32, int poly, int dk, int dv) {
-  return !f32 && poly != POLY_GEN2 && dk % 64 == 0 && dv % 64 == 0;
+  return !f32 && !two_pair_poly(poly) && dk % 64 == 0 && dv % 64 == 0;
 }
 
 template <typename T, int POLY, int DK, int DV> hipError_t launch_fwd(const KParams& p, hipStream_t st);
