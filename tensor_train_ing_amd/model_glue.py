@@ -1,0 +1,57 @@
+"""Model-side hooks for the "hip" attention backend.
+
+The reference model prepares its fast path in `make_ctx` (ref: tnlm/model.py:205-227): with a fast backend it builds
+no T x T mask, only the per-query row scales n_visible^-p (n_visible = position in document + 1, 0 for padding;
+ref: tnlm/model.py:217-221), and `Attention.forward` hands them to the operator (ref: tnlm/model.py:86-91). These
+functions do the same for "hip", so the reference's model code needs only its backend test widened
+(INTEGRATION.md shows the patch). `source_sha256` extends the checkpoint's source identity
+(ref: tnlm/checkpoint.py:54) with this package's kernel sources.
+"""
+from __future__ import annotations
+
+import hashlib
+from pathlib import Path
+
+import torch
+
+from .config import poly_attention_for
+
+PKG = Path(__file__).resolve().parent
+
+
+def row_scales(doc_ids: torch.Tensor, positions: torch.Tensor, powers) -> dict:
+    """{p: (B, T) float32}: (position + 1)^-p for real tokens (doc id >= 0), 0 for padding. `positions` is the
+    model's position within document (ref: tnlm/attention.py:12-19). This equals n_visible^-p for contiguous
+    documents, which the kernels assume.  ref: tnlm/model.py:217-221"""
+    n = (positions + 1).float()
+    valid = doc_ids >= 0
+    return {p: torch.where(valid, n.pow(-p), torch.zeros_like(n)) for p in powers}
+
+
+def fast_context(doc_ids: torch.Tensor, positions: torch.Tensor, powers, backend: str = "hip") -> dict:
+    """The fast-path part of the model context: doc ids, backend name and row scales (no visibility mask)."""
+    return {"doc_ids": doc_ids, "backend": backend, "row_scale": row_scales(doc_ids, positions, powers)}
+
+
+def attention(kind: str, q1, k1, q2, k2, v, ctx: dict, row_power: float, coef=None, b=None, degree=None):
+    """Attention.forward's fast-path call (ref: tnlm/model.py:86-91) for ctx["backend"] == "hip": (B, H, T, dv)."""
+    fn = poly_attention_for(ctx["backend"])
+    kw = {"degree": degree} if kind == "power" else {}
+    return fn(kind, q1, k1, q2, k2, v, ctx["doc_ids"], ctx["row_scale"][row_power], coef=coef, b=b, **kw)
+
+
+def source_files() -> list[Path]:
+    """Every source file the operator is built from or runs: the Python package, the HIP kernels and the C ABI
+    header (the built library is excluded)."""
+    files = sorted(PKG.rglob("*.py")) + sorted((PKG / "csrc").glob("*.hip")) + sorted((PKG / "csrc").glob("*.hpp"))
+    header = PKG.parent / "include" / "tnpa.h"
+    if header.exists():
+        files.append(header)
+    return [f for f in files if "_build" not in f.parts and "__pycache__" not in f.parts]
+
+
+def source_sha256() -> dict:
+    """{"tensor_train_ing_amd/<path>": sha256 hex} for source_files(), in the form of the reference checkpoint's
+    `source_sha256` entries (ref: tnlm/checkpoint.py:54), to be merged into them."""
+    root = PKG.parent
+    return {f.relative_to(root).as_posix(): hashlib.sha256(f.read_bytes()).hexdigest() for f in source_files()}

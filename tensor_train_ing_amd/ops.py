@@ -1,0 +1,104 @@
+"""The polynomial attention as registered torch custom ops, for callers that compile their model.
+
+The reference trains a compiled model (ref: tnlm/train.py:353); its Triton operator is traced through. A ctypes
+call cannot be traced, so the same HIP kernels are registered here as two opaque custom ops with fake (shape)
+implementations and an autograd formula:
+
+    tnpa::poly_attention           (kind, degree, q1, k1, q2?, k2?, v, doc_ids, row_scale, coef?, b?)
+                                   -> (o, doc_start, query_end)
+    tnpa::poly_attention_backward  (kind, degree, q1, k1, q2?, k2?, v, doc_start, query_end, row_scale, coef?, b?, dO)
+                                   -> (dq1, dk1, dq2, dk2, dv, dpar)
+
+Outputs and gradients are contiguous (B, H, T, d); dq2/dk2 are empty for one-pair kinds and dpar is empty unless the
+kind has head parameters. The document bounds computed by the forward are handed to the backward, as the
+reference's autograd.Function saves its LO/HI (ref: tnlm/kernels/poly_attn.py:281).
+`poly_attention_hip` switches to these ops by itself while torch.compile traces it.
+"""
+from typing import Optional
+
+import torch
+
+from . import _abi
+from .poly_attn import _canonical, _prep, _run_backward, _run_forward
+
+_PAR_KINDS = (_abi.OFFSET_SQUARE, _abi.LOWER_DEGREE_MIX)
+_TWO_PAIRS = (_abi.SIGNED_PRODUCT, _abi.LOWER_DEGREE_MIX)
+
+
+@torch.library.custom_op("tnpa::poly_attention", mutates_args=())
+def _fwd(kind: int, degree: int, q1: torch.Tensor, k1: torch.Tensor, q2: Optional[torch.Tensor],
+         k2: Optional[torch.Tensor], v: torch.Tensor, doc_ids: torch.Tensor, row_scale: torch.Tensor,
+         coef: Optional[torch.Tensor], b: Optional[torch.Tensor]) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
+    o, dstart, qend, *_ = _run_forward(kind, degree if degree > 0 else None, q1, k1, q2, k2, v, doc_ids, row_scale,
+                                       coef, b, out_like_v=False)
+    return o, dstart, qend
+
+
+@_fwd.register_fake
+def _fwd_fake(kind, degree, q1, k1, q2, k2, v, doc_ids, row_scale, coef, b):
+    B, T = doc_ids.shape
+    o = v.new_empty(v.shape)
+    return o, doc_ids.new_empty((B, T), dtype=torch.int32), doc_ids.new_empty((B, T), dtype=torch.int32)
+
+
+@torch.library.custom_op("tnpa::poly_attention_backward", mutates_args=())
+def _bwd(kind: int, degree: int, q1: torch.Tensor, k1: torch.Tensor, q2: Optional[torch.Tensor],
+         k2: Optional[torch.Tensor], v: torch.Tensor, doc_start: torch.Tensor, query_end: torch.Tensor,
+         row_scale: torch.Tensor, coef: Optional[torch.Tensor], b: Optional[torch.Tensor],
+         dout: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor, torch.Tensor, torch.Tensor,
+                                      torch.Tensor]:
+    two = kind in _TWO_PAIRS
+    q1, k1, v = _prep(q1), _prep(k1), _prep(v)
+    q2, k2 = (_prep(q2), _prep(k2)) if two else (q1, k1)
+    sc = row_scale.detach().float().contiguous()
+    coef_f = coef.detach().float().contiguous() if kind == _abi.LOWER_DEGREE_MIX else None
+    b_f = b.detach().float().contiguous() if kind == _abi.OFFSET_SQUARE else None
+    dq1, dk1, dq2, dk2, dv, dpar = _run_backward(kind, degree if degree > 0 else None, q1, k1, q2, k2, v,
+                                                 doc_start, query_end, sc, coef_f, b_f, dout,
+                                                 grads_like_inputs=False)
+    # one-pair kinds: distinct empty tensors (custom-op outputs may not alias each other)
+    return (dq1, dk1, dq2 if two else q1.new_empty(0), dk2 if two else q1.new_empty(0), dv,
+            dpar if dpar is not None else q1.new_empty(0, dtype=torch.float32))
+
+
+@_bwd.register_fake
+def _bwd_fake(kind, degree, q1, k1, q2, k2, v, doc_start, query_end, row_scale, coef, b, dout):
+    two = kind in _TWO_PAIRS
+    H = q1.shape[1]
+    return (q1.new_empty(q1.shape), k1.new_empty(k1.shape), q2.new_empty(q2.shape) if two else q1.new_empty(0),
+            k2.new_empty(k2.shape) if two else q1.new_empty(0), v.new_empty(v.shape),
+            q1.new_empty((H, 4), dtype=torch.float32) if kind in _PAR_KINDS else q1.new_empty(0, dtype=torch.float32))
+
+
+def _setup_context(ctx, inputs, output):
+    kind, degree, q1, k1, q2, k2, v, doc_ids, row_scale, coef, b = inputs
+    _, dstart, qend = output
+    ctx.kind, ctx.degree = kind, degree
+    ctx.coef_dtype = coef.dtype if coef is not None else None
+    ctx.b_dtype = b.dtype if b is not None else None
+    ctx.save_for_backward(q1, k1, q2, k2, v, dstart, qend, row_scale, coef, b)
+
+
+def _backward(ctx, do, _dstart_grad, _qend_grad):
+    q1, k1, q2, k2, v, dstart, qend, row_scale, coef, b = ctx.saved_tensors
+    kind = ctx.kind
+    dq1, dk1, dq2, dk2, dv, dpar = _bwd(kind, ctx.degree, q1, k1, q2, k2, v, dstart, qend, row_scale, coef, b,
+                                        do.contiguous())
+    two = kind in _TWO_PAIRS
+    dcoef = dpar.to(ctx.coef_dtype) if (kind == _abi.LOWER_DEGREE_MIX and coef is not None) else None
+    db = dpar[:, 0].to(ctx.b_dtype) if (kind == _abi.OFFSET_SQUARE and b is not None) else None
+    return (None, None, dq1, dk1, dq2 if two else None, dk2 if two else None, dv, None, None, dcoef, db)
+
+
+_fwd.register_autograd(_backward, setup_context=_setup_context)
+
+
+def poly_attention_op(kind, q1, k1, q2, k2, v, doc_ids, row_scale, coef=None, b=None, *, degree=None):
+    """poly_attention_hip through the registered custom ops (same arguments, same results; contiguous output).
+    Unknown kinds raise KeyError, as the reference."""
+    K, degree = _canonical(kind, q1, k1, q2, k2, degree)
+    two = K in _TWO_PAIRS
+    o, _, _ = _fwd(K, int(degree) if degree is not None else 0, q1, k1, q2 if two else None, k2 if two else None,
+                   v, doc_ids, row_scale, coef if K == _abi.LOWER_DEGREE_MIX else None,
+                   b if K == _abi.OFFSET_SQUARE else None)
+    return o

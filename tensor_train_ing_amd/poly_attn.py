@@ -111,35 +111,79 @@ def _validate(K, q1, k1, q2, k2, v, doc_ids, row_scale, coef, b, degree):
         raise ValueError("power kind needs degree in 1..8")
 
 
+def _canonical(kind, q1, k1, q2, k2, degree):
+    """(kind code, degree): signed_product with shared pairs (q2 is q1 and k2 is k1) is degree-2 power."""
+    K = KINDS[kind]  # unknown kind -> KeyError, as the reference
+    if K == _abi.SIGNED_PRODUCT and q2 is q1 and k2 is k1:
+        return _abi.POWER, 2
+    return K, degree
+
+
+def _run_forward(K, degree, q1, k1, q2, k2, v, doc_ids, row_scale, coef, b, out_like_v=True):
+    """Validates, computes the document bounds and launches the forward. Returns (o, dstart, qend, (q1, k1, q2, k2,
+    v) as the kernels read them, sc, coef_f, b_f). o has v's strides (out_like_v) or is contiguous."""
+    _validate(K, q1, k1, q2, k2, v, doc_ids, row_scale, coef, b, degree)
+    q1, k1, v = _prep(q1), _prep(k1), _prep(v)
+    if K in _TWO_PAIRS:
+        q2, k2 = _prep(q2), _prep(k2)
+    else:
+        q2, k2 = q1, k1
+    dstart, qend = doc_bounds(doc_ids)
+    sc = row_scale.detach().float().contiguous()
+    coef_f = coef.detach().float().contiguous() if K == _abi.LOWER_DEGREE_MIX else None
+    b_f = b.detach().float().contiguous() if K == _abi.OFFSET_SQUARE else None
+    o = torch.empty_like(v) if out_like_v else None
+    if o is None or not _aligned_rows(o):
+        o = torch.empty(v.shape, dtype=v.dtype, device=v.device)
+    prob = _problem(K, degree, q1, k1, q2, k2, v, dstart, qend, sc, coef_f, b_f)
+    lib = _abi.load()
+    with torch.cuda.device(q1.device):
+        _abi.check(lib.tnpa_forward(ctypes.byref(prob), ctypes.byref(_desc(o)), _stream(q1.device)),
+                   "poly_attention forward")
+    return o, dstart, qend, (q1, k1, q2, k2, v), sc, coef_f, b_f
+
+
+def _run_backward(K, degree, q1, k1, q2, k2, v, dstart, qend, sc, coef_f, b_f, do, grads_like_inputs=True):
+    """Launches the backward on tensors prepared by _run_forward. Returns (dq1, dk1, dq2, dk2, dv, dpar), with
+    dq2/dk2 None for one-pair kinds and dpar the (H, 4) fp32 head-parameter gradient or None."""
+    H = q1.shape[1]
+    do = _prep(do.to(v.dtype))
+    alloc = _alloc_like if grads_like_inputs else (lambda x: torch.empty(x.shape, dtype=x.dtype, device=x.device))
+    dq1, dk1, dv = alloc(q1), alloc(k1), alloc(v)
+    two = K in _TWO_PAIRS
+    dq2, dk2 = (alloc(q2), alloc(k2)) if two else (dq1, dk1)
+    prob = _problem(K, degree, q1, k1, q2, k2, v, dstart, qend, sc, coef_f, b_f)
+    lib = _abi.load()
+    par = K in (_abi.OFFSET_SQUARE, _abi.LOWER_DEGREE_MIX)
+    ws = dpar = None
+    if par:
+        ws = torch.empty(max(1, lib.tnpa_dpar_workspace_floats(ctypes.byref(prob))), dtype=torch.float32,
+                         device=q1.device)
+        dpar = torch.empty(H, 4, dtype=torch.float32, device=q1.device)
+    # row_scale * dO, written by the library before its dK/dV pass and streamed by it, where that beats the pass
+    # scaling dO itself
+    dos = (torch.empty(do.shape, dtype=do.dtype, device=do.device)
+           if lib.tnpa_dout_scaled_helps(ctypes.byref(prob)) else None)
+    g = _abi.Grads(_desc(do), _desc(dq1), _desc(dk1), _desc(dq2), _desc(dk2), _desc(dv),
+                   ws.data_ptr() if par else None, dpar.data_ptr() if par else None,
+                   _desc(dos) if dos is not None else _abi.Tensor())
+    with torch.cuda.device(q1.device):
+        _abi.check(lib.tnpa_backward(ctypes.byref(prob), ctypes.byref(g), _stream(q1.device)),
+                   "poly_attention backward")
+    if not two:
+        dq2 = dk2 = None
+    return dq1, dk1, dq2, dk2, dv, dpar
+
+
 class PolyAttention(torch.autograd.Function):
     """ref: tnlm/kernels/poly_attn.py:255-309, with an appended `degree` argument for kind="power"."""
 
     @staticmethod
     def forward(ctx, kind, q1, k1, q2, k2, v, doc_ids, row_scale, coef, b, degree=None):
-        K = KINDS[kind]  # unknown kind -> KeyError, as the reference
-        shared = K == _abi.SIGNED_PRODUCT and q2 is q1 and k2 is k1
-        if shared:
-            K, degree = _abi.POWER, 2
-        _validate(K, q1, k1, q2, k2, v, doc_ids, row_scale, coef, b, degree)
-        B, H, T, DK = q1.shape
-        DV = v.shape[-1]
-        q1, k1, v = _prep(q1), _prep(k1), _prep(v)
-        if K in _TWO_PAIRS:
-            q2, k2 = _prep(q2), _prep(k2)
-        else:
-            q2, k2 = q1, k1
-        dstart, qend = doc_bounds(doc_ids)
-        sc = row_scale.detach().float().contiguous()
-        coef_f = coef.detach().float().contiguous() if K == _abi.LOWER_DEGREE_MIX else None
-        b_f = b.detach().float().contiguous() if K == _abi.OFFSET_SQUARE else None
-        o = torch.empty_like(v)
-        if not _aligned_rows(o):
-            o = torch.empty(v.shape, dtype=v.dtype, device=v.device)
-        prob = _problem(K, degree, q1, k1, q2, k2, v, dstart, qend, sc, coef_f, b_f)
-        lib = _abi.load()
-        with torch.cuda.device(q1.device):
-            _abi.check(lib.tnpa_forward(ctypes.byref(prob), ctypes.byref(_desc(o)), _stream(q1.device)),
-                       "poly_attention forward")
+        shared = KINDS[kind] == _abi.SIGNED_PRODUCT and q2 is q1 and k2 is k1
+        K, degree = _canonical(kind, q1, k1, q2, k2, degree)
+        o, dstart, qend, (q1, k1, q2, k2, v), sc, coef_f, b_f = _run_forward(
+            K, degree, q1, k1, q2, k2, v, doc_ids, row_scale, coef, b)
         ctx.save_for_backward(q1, k1, q2, k2, v, dstart, qend, sc, coef_f, b_f)
         ctx.K, ctx.degree, ctx.shared = K, degree, shared
         ctx.has_coef, ctx.has_b = coef is not None, b is not None
@@ -151,33 +195,10 @@ class PolyAttention(torch.autograd.Function):
     def backward(ctx, do):
         q1, k1, q2, k2, v, dstart, qend, sc, coef_f, b_f = ctx.saved_tensors
         K = ctx.K
-        H = q1.shape[1]
-        do = _prep(do.to(v.dtype))
-        dq1, dk1, dv = _alloc_like(q1), _alloc_like(k1), _alloc_like(v)
-        two = K in _TWO_PAIRS
-        dq2, dk2 = (_alloc_like(q2), _alloc_like(k2)) if two else (dq1, dk1)
-        prob = _problem(K, ctx.degree, q1, k1, q2, k2, v, dstart, qend, sc, coef_f, b_f)
-        lib = _abi.load()
-        par = K in (_abi.OFFSET_SQUARE, _abi.LOWER_DEGREE_MIX)
-        ws = dpar = None
-        if par:
-            ws = torch.empty(max(1, lib.tnpa_dpar_workspace_floats(ctypes.byref(prob))), dtype=torch.float32,
-                             device=q1.device)
-            dpar = torch.empty(H, 4, dtype=torch.float32, device=q1.device)
-        # row_scale * dO, written by the library before its dK/dV pass and streamed by it, where that beats the pass
-        # scaling dO itself
-        dos = (torch.empty(do.shape, dtype=do.dtype, device=do.device)
-               if lib.tnpa_dout_scaled_helps(ctypes.byref(prob)) else None)
-        g = _abi.Grads(_desc(do), _desc(dq1), _desc(dk1), _desc(dq2), _desc(dk2), _desc(dv),
-                       ws.data_ptr() if par else None, dpar.data_ptr() if par else None,
-                       _desc(dos) if dos is not None else _abi.Tensor())
-        with torch.cuda.device(q1.device):
-            _abi.check(lib.tnpa_backward(ctypes.byref(prob), ctypes.byref(g), _stream(q1.device)),
-                       "poly_attention backward")
+        dq1, dk1, dq2, dk2, dv, dpar = _run_backward(K, ctx.degree, q1, k1, q2, k2, v, dstart, qend, sc, coef_f,
+                                                      b_f, do)
         dcoef = dpar.to(ctx.coef_dtype) if (K == _abi.LOWER_DEGREE_MIX and ctx.has_coef) else None
         db = dpar[:, 0].to(ctx.b_dtype) if (K == _abi.OFFSET_SQUARE and ctx.has_b) else None
-        if not two:
-            dq2 = dk2 = None
         return None, dq1, dk1, dq2, dk2, dv, None, None, dcoef, db, None
 
 
@@ -199,4 +220,8 @@ def poly_attention_hip(kind, q1, k1, q2, k2, v, doc_ids, row_scale, coef=None, b
     """q*, k*: (B, H, T, dk); v: (B, H, T, dv); doc_ids: (B, T) contiguous ids, < 0 = padding;
     row_scale: (B, T) = n_visible^-p for real queries, 0 for padding. kind="power" takes degree=p and ignores
     q2/k2. Every gradient is reduced in a fixed order (deterministic).  ref: tnlm/kernels/poly_attn.py:312-315"""
+    if torch.compiler.is_compiling():
+        # under torch.compile the same kernels run behind registered custom ops (opaque to the compiler)
+        from .ops import poly_attention_op
+        return poly_attention_op(kind, q1, k1, q2, k2, v, doc_ids, row_scale, coef, b, degree=degree)
     return PolyAttention.apply(kind, q1, k1, q2, k2, v, doc_ids, row_scale, coef, b, degree)

@@ -1,0 +1,106 @@
+"""Full-model parity through the "hip" backend, and the compiled (custom-op) path.
+
+Mirrors ref: tests/test_kernels.py:106-125: the same two-layer model with the dense reference attention and with
+the fast operator, documents and padding in the batch, loss within 1e-4 * |loss| and every parameter gradient
+within 1e-3 (relative Frobenius norm), float32.
+"""
+from __future__ import annotations
+
+import pytest
+import torch
+
+from mini_lm import MiniLM
+
+pytestmark = pytest.mark.gpu
+
+
+def _rel(x, ref):
+    return ((x.float() - ref.float()).norm() / ref.float().norm().clamp(min=1e-30)).item()
+
+
+def _batch(dev):
+    g = torch.Generator().manual_seed(0)
+    idx = torch.randint(0, 97, (2, 100), generator=g).to(dev)
+    doc = torch.zeros(2, 100, dtype=torch.long, device=dev)
+    doc[0, 30:] = 1
+    doc[1, 90:] = -1
+    tgt = idx.roll(-1, 1).masked_fill(doc < 0, -100)
+    return idx, doc, tgt
+
+
+def _pair(kind, mlp, dev, degree=2):
+    torch.manual_seed(0)
+    ref = MiniLM(kind, mlp, backend="reference", degree=degree).to(dev)
+    hip = MiniLM(kind, mlp, backend="hip", degree=degree).to(dev)
+    hip.load_state_dict(ref.state_dict())
+    return ref, hip
+
+
+@pytest.mark.parametrize("kind,mlp", [("signed_product", "bilinear"), ("offset_square", "bilinear"),
+                                      ("lower_degree_mix", "affine_bilinear"), ("power", "bilinear")])
+def test_model_hip_backend_matches_reference(kind, mlp):
+    dev = torch.device("cuda:0")
+    print(f"[model parity] kind={kind} mlp={mlp} B2 T100 fp32", flush=True)
+    ref, hip = _pair(kind, mlp, dev)
+    idx, doc, tgt = _batch(dev)
+    _, lr = ref(idx, doc, tgt)
+    lr.backward()
+    _, lh = hip(idx, doc, tgt)
+    lh.backward()
+    torch.cuda.synchronize()
+    assert abs(lr.item() - lh.item()) < 1e-4 * abs(lr.item())
+    for (n, a), (_, b) in zip(ref.named_parameters(), hip.named_parameters()):
+        assert b.grad is not None, n
+        assert _rel(b.grad, a.grad) < 1e-3, (n, _rel(b.grad, a.grad))
+
+
+@pytest.mark.parametrize("kind", ["signed_product", "offset_square", "power"])
+def test_compiled_model_matches_eager(kind):
+    """torch.compile(fullgraph=True) traces the model with the operator as opaque tnpa:: custom ops (a graph break
+    would raise); loss and gradients equal the eager run's."""
+    dev = torch.device("cuda:0")
+    print(f"[compiled model] kind={kind}", flush=True)
+    torch._dynamo.reset()
+    _, eager = _pair(kind, "bilinear", dev)
+    _, comp = _pair(kind, "bilinear", dev)
+    idx, doc, tgt = _batch(dev)
+    _, le = eager(idx, doc, tgt)
+    le.backward()
+    fn = torch.compile(comp, backend="aot_eager", fullgraph=True)
+    _, lc = fn(idx, doc, tgt)
+    lc.backward()
+    torch.cuda.synchronize()
+    assert abs(le.item() - lc.item()) <= 1e-6 * abs(le.item())
+    for (n, a), (_, b) in zip(eager.named_parameters(), comp.named_parameters()):
+        assert _rel(b.grad, a.grad) < 1e-5, (n, _rel(b.grad, a.grad))
+
+
+@pytest.mark.parametrize("kind", ["signed_product", "offset_square", "lower_degree_mix", "power"])
+def test_custom_op_equals_autograd_function(kind):
+    """The custom-op path launches the same kernels: bit-identical output and gradients (bf16, documents)."""
+    from poly_ref import gaussian_inputs, row_scale
+    from tensor_train_ing_amd import poly_attention_hip, poly_attention_op
+    dev = torch.device("cuda:0")
+    print(f"[custom op] kind={kind}", flush=True)
+    two = kind in ("signed_product", "lower_degree_mix")
+    q1, k1, q2, k2, v, do = (x.to(dev) for x in gaussian_inputs(2, 3, 200, 64, 64, torch.bfloat16, 5,
+                                                                 qk_scale=64 ** -0.25, two_pairs=True))
+    doc = torch.zeros(2, 200, dtype=torch.long, device=dev)
+    doc[0, 70:] = 1
+    doc[1, 150:] = -1
+    rs = row_scale(doc, 0.5)
+    coef = torch.tensor([[0.1, 0.2, -0.3, 1.0]], device=dev).repeat(3, 1) if kind == "lower_degree_mix" else None
+    b = torch.full((3,), 0.5, device=dev) if kind == "offset_square" else None
+    outs = []
+    for fn in (poly_attention_hip, poly_attention_op):
+        ins = [x.detach().clone().requires_grad_() for x in (q1, k1, q2, k2, v)]
+        par = [t.detach().clone().requires_grad_() if t is not None else None for t in (coef, b)]
+        o = fn(kind, ins[0], ins[1], ins[2] if two else None, ins[3] if two else None, ins[4], doc, rs,
+               coef=par[0], b=par[1], degree=2 if kind == "power" else None)
+        o.backward(do)
+        grads = [t.grad for t in ins if t.grad is not None] + [t.grad for t in par if t is not None]
+        outs.append([o.detach()] + grads)
+    torch.cuda.synchronize()
+    assert len(outs[0]) == len(outs[1])
+    for a, b_ in zip(*outs):
+        assert torch.equal(a, b_)
