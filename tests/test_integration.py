@@ -80,3 +80,12 @@ def test_no_cpu_fallback():
     for fn in (poly_attention_hip, poly_attention_op):
         with pytest.raises(ValueError, match="ROCm device"):
             fn("power", q, q, None, None, q, doc, rs, degree=2)
+
+
+@pytest.mark.parametrize("T,L", [(128, 0), (128, 128), (100, 30), (97, 7), (64, 1), (50, 200)])
+def test_bench_counts_exactly_the_visible_pairs(T, L):
+    """bench.py's FLOP count uses the number of visible (query, key) pairs; brute force over the dense mask."""
+    import bench
+    from oracle import visible_mask
+    doc = (np.arange(T) // L if L else np.zeros(T, dtype=np.int64))[None].astype(np.int64)
+    assert bench.npairs(T, L) == int(visible_mask(doc).sum())
