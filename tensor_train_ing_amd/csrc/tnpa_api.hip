@@ -362,7 +362,8 @@ int tnpa_forward(const tnpa_problem_t* problem, const tnpa_tensor_t* out, void* 
 int64_t tnpa_dpar_workspace_floats(const tnpa_problem_t* problem) {
   if (problem == nullptr) return 0;
   if (problem->kind != TNPA_OFFSET_SQUARE && problem->kind != TNPA_LOWER_DEGREE_MIX) return 0;
-  const int bk = tnpa::kv_block_keys(problem->dtype == TNPA_F32, poly_of(*problem));
+  const int bk = tnpa::kv_block_keys(problem->dtype == TNPA_F32, poly_of(*problem), problem->head_dim_k,
+                                     problem->head_dim_v);
   const int64_t nnb = (problem->seq_len + bk - 1) / bk;
   return (int64_t)problem->batch * problem->heads * nnb * 4;
 }
@@ -445,7 +446,7 @@ int tnpa_backward_phase(const tnpa_problem_t* problem, const tnpa_grads_t* grads
     if (e != hipSuccess) return fail(TNPA_ERR_LAUNCH, "tnpa_backward (dQ): %s", hipGetErrorString(e));
   }
   if (par) {
-    const int bk = tnpa::kv_block_keys(p.dtype == TNPA_F32, poly_of(p));
+    const int bk = tnpa::kv_block_keys(p.dtype == TNPA_F32, poly_of(p), p.head_dim_k, p.head_dim_v);
     const int nnb = (p.seq_len + bk - 1) / bk;
     const int n = p.heads * 4;
     hipLaunchKernelGGL(k_dpar_reduce, dim3((n + 255) / 256), dim3(256), 0, (hipStream_t)stream, grads->dpar_partial,

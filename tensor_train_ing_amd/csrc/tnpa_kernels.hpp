@@ -133,10 +133,14 @@ template <typename T, int POLY, int DK, int DV> struct Cfg {
   static constexpr int NPAIR = two_pair_poly(POLY) ? 2 : 1;
   // two waves per SIMD (16-bit, one pair): eight waves per workgroup, so each staged tile serves 256 rows
   static constexpr bool TWO = !F32 && NPAIR == 1;
-  static constexpr int FW_NW = TWO ? 8 : 4, FW_QW = 1, FW_BN = F32 ? 32 : 64, FW_WPE = TWO ? 2 : 1;
-  static constexpr int BQ_NW = TWO ? 8 : 4, BQ_QW = 1, BQ_BN = F32 ? 32 : 64, BQ_WPE = TWO ? 2 : 1;
+  // Head dims up to 64: four-wave workgroups, two per CU (their LDS fits twice), so one workgroup's barrier waits,
+  // prologue and epilogue overlap the other's MFMA work. Larger head dims: one eight-wave workgroup per CU.
+  static constexpr bool SMALL = TWO && DK <= 64 && DV <= 64;
+  static constexpr int NW2 = SMALL ? 4 : 8;
+  static constexpr int FW_NW = TWO ? NW2 : 4, FW_QW = 1, FW_BN = F32 ? 32 : 64, FW_WPE = TWO ? 2 : 1;
+  static constexpr int BQ_NW = TWO ? NW2 : 4, BQ_QW = 1, BQ_BN = F32 ? 32 : 64, BQ_WPE = TWO ? 2 : 1;
   static constexpr bool KV_SPLIT = TWO;  // separate dV and dK passes at two waves per SIMD
-  static constexpr int KV_NW = KV_SPLIT ? 8 : 4, KV_KW = 1, KV_BM = F32 ? 32 : 64, KV_WPE = 1;
+  static constexpr int KV_NW = KV_SPLIT ? NW2 : 4, KV_KW = 1, KV_BM = F32 ? 32 : 64, KV_WPE = 1;
   static constexpr int KV_KEYS = KV_NW * KV_KW * 32;
 };
 
@@ -1242,7 +1246,7 @@ template <typename T, int POLY, int DK, int DV> hipError_t launch_fwd(const KPar
 
 template <typename T, int POLY, int DK, int DV> hipError_t launch_bwd_kv(const KParams& p, hipStream_t st) {
   typedef Cfg<T, POLY, DK, DV> C;
-  static_assert(C::KV_KEYS == (C::KV_SPLIT ? 256 : 128), "dK/dV block size mirrors kv_block_keys()");
+  static_assert(C::KV_KEYS == (C::KV_SPLIT && !C::SMALL ? 256 : 128), "dK/dV block size mirrors kv_block_keys()");
   const int grid = p.B * p.H * ((p.T + C::KV_KEYS - 1) / C::KV_KEYS);
   if constexpr (C::KV_SPLIT) {
     if (p.kvsel & 1)

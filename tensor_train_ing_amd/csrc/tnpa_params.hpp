@@ -43,14 +43,18 @@ struct KParams {
 inline bool kv_split(bool f32, int poly) { return !f32 && !two_pair_poly(poly); }
 
 // Keys per dK/dV workgroup (sizes the dcoef/db partials); mirrors Cfg::KV_KEYS: eight waves of 32 keys for the split
-// passes (two waves per SIMD), four for the one-wave-per-SIMD combined kernel.
-inline int kv_block_keys(bool f32, int poly) { return kv_split(f32, poly) ? 256 : 128; }
+// passes (two waves per SIMD) with head dims above 64, four waves otherwise.
+inline int kv_block_keys(bool f32, int poly, int dk, int dv) {
+  return kv_split(f32, poly) && (dk > 64 || dv > 64) ? 256 : 128;
+}
 
 // Whether the dK/dV passes scale dO by the row scale themselves at no cost: they stage the dO rows a step ahead and
-// apply the factor when writing them to LDS (three-buffer staging; 16-bit inputs, one q/k pair, head dims that
-// are multiples of 64). Then a separate pre-scaling pass costs more than it saves. Mirrors k_bwd_kv's NBUF == 3.
+// apply the factor when writing them to LDS (three-buffer staging; 16-bit inputs, one q/k pair, and 64-row tiles
+// of q and dO that split into whole 16-byte chunks per thread: 8*d chunks over 256 threads for head dims up to 64,
+// 512 threads above). Then a separate pre-scaling pass costs more than it saves. Mirrors k_bwd_kv's NBUF == 3.
 constexpr bool kv_scales_in_pass(bool f32, int poly, int dk, int dv) {
-  return !f32 && !two_pair_poly(poly) && dk % 64 == 0 && dv % 64 == 0;
+  const int nt = dk <= 64 && dv <= 64 ? 256 : 512;
+  return !f32 && !two_pair_poly(poly) && (8 * dk) % nt == 0 && (8 * dv) % nt == 0;
 }
 
 template <typename T, int POLY, int DK, int DV> hipError_t launch_fwd(const KParams& p, hipStream_t st);

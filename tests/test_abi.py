@@ -143,20 +143,26 @@ def test_dpar_workspace_size(lib):
     assert lib.tnpa_dpar_workspace_floats(ctypes.byref(_problem())) == 0
     p = _problem(kind=_abi.LOWER_DEGREE_MIX, seq_len=300)
     assert lib.tnpa_dpar_workspace_floats(ctypes.byref(p)) == 2 * 2 * 3 * 4  # ceil(300 / 128) key blocks
-    p = _problem(kind=_abi.OFFSET_SQUARE, seq_len=300)  # bf16, one pair: split passes with 256-key blocks
+    p = _problem(kind=_abi.OFFSET_SQUARE, seq_len=300)  # bf16, one pair, head dim 64: four-wave 128-key blocks
+    assert lib.tnpa_dpar_workspace_floats(ctypes.byref(p)) == 2 * 2 * 3 * 4
+    p = _problem(kind=_abi.OFFSET_SQUARE, seq_len=300, head_dim_k=128, head_dim_v=128)  # eight-wave 256-key blocks
     assert lib.tnpa_dpar_workspace_floats(ctypes.byref(p)) == 2 * 2 * 2 * 4
 
 
 def test_dout_scaled_helps_only_where_the_passes_cannot_scale_for_free(lib):
     from tensor_train_ing_amd import _abi
     assert lib.tnpa_dout_scaled_helps(None) == 0
-    # 16-bit, one q/k pair, head dims multiples of 64: the dK/dV passes scale dO as they write it to LDS
+    # 16-bit, one q/k pair, tiles that split evenly over the threads (head dims 32 or 64 with four-wave workgroups,
+    # 64 or 128 with eight-wave ones): the dK/dV passes scale dO as they write it to LDS
     assert lib.tnpa_dout_scaled_helps(ctypes.byref(_problem())) == 0
     assert lib.tnpa_dout_scaled_helps(ctypes.byref(_problem(dtype=_abi.F16, kind=_abi.OFFSET_SQUARE))) == 0
-    # fp32, two q/k pairs, or a head dim below 64: the pre-scaled workspace is faster
+    assert lib.tnpa_dout_scaled_helps(ctypes.byref(_problem(head_dim_v=32))) == 0
+    assert lib.tnpa_dout_scaled_helps(ctypes.byref(_problem(head_dim_k=128, head_dim_v=128))) == 0
+    # fp32, two q/k pairs, or a head dim too small for the tile split: the pre-scaled workspace is faster
     assert lib.tnpa_dout_scaled_helps(ctypes.byref(_problem(dtype=_abi.F32))) == 1
     assert lib.tnpa_dout_scaled_helps(ctypes.byref(_problem(kind=_abi.SIGNED_PRODUCT))) == 1
-    assert lib.tnpa_dout_scaled_helps(ctypes.byref(_problem(head_dim_v=32))) == 1
+    assert lib.tnpa_dout_scaled_helps(ctypes.byref(_problem(head_dim_v=16))) == 1
+    assert lib.tnpa_dout_scaled_helps(ctypes.byref(_problem(head_dim_k=128, head_dim_v=32))) == 1
 
 
 def test_python_operator_errors_mirror_the_reference():
