@@ -137,8 +137,13 @@ template <typename T, int POLY, int DK, int DV> struct Cfg {
   // prologue and epilogue overlap the other's MFMA work. Larger head dims: one eight-wave workgroup per CU.
   static constexpr bool SMALL = TWO && DK <= 64 && DV <= 64;
   static constexpr int NW2 = SMALL ? 4 : 8;
-  static constexpr int FW_NW = TWO ? NW2 : 4, FW_QW = 1, FW_BN = F32 ? 32 : 64, FW_WPE = TWO ? 2 : 1;
-  static constexpr int BQ_NW = TWO ? NW2 : 4, BQ_QW = 1, BQ_BN = F32 ? 32 : 64, BQ_WPE = TWO ? 2 : 1;
+  // Two q/k pairs, 16-bit, head dims up to 64: the forward and dQ kernels fit 256 registers too (two waves per
+  // SIMD, eight-wave workgroups); at head dim 128 they need one wave per SIMD (the forward would spill 93 registers).
+  static constexpr bool PAIR2_TWO = !F32 && NPAIR == 2 && DK <= 64 && DV <= 64;
+  static constexpr int FW_NW = TWO ? NW2 : PAIR2_TWO ? 8 : 4, FW_QW = 1, FW_BN = F32 ? 32 : 64;
+  static constexpr int FW_WPE = TWO || PAIR2_TWO ? 2 : 1;
+  static constexpr int BQ_NW = TWO ? NW2 : PAIR2_TWO ? 8 : 4, BQ_QW = 1, BQ_BN = F32 ? 32 : 64;
+  static constexpr int BQ_WPE = TWO || PAIR2_TWO ? 2 : 1;
   static constexpr bool KV_SPLIT = TWO;  // separate dV and dK passes at two waves per SIMD
   static constexpr int KV_NW = KV_SPLIT ? NW2 : 4, KV_KW = 1, KV_BM = F32 ? 32 : 64, KV_WPE = 1;
   static constexpr int KV_KEYS = KV_NW * KV_KW * 32;
