@@ -138,10 +138,13 @@ template <typename T, int POLY, int DK, int DV> struct Cfg {
   static constexpr bool SMALL = TWO && DK <= 64 && DV <= 64;
   static constexpr int NW2 = SMALL ? 4 : 8;
   // Two q/k pairs, 16-bit, head dims up to 64: the forward and dQ kernels fit 256 registers too (two waves per
-  // SIMD, eight-wave workgroups); at head dim 128 they need one wave per SIMD (the forward would spill 93 registers).
+  // SIMD, eight-wave workgroups). At head dim 128 the signed_product forward does so without its software pipeline
+  // (two staging buffers; 16 registers spilled, still 19% faster than one wave per SIMD); lower_degree_mix's would
+  // spill 315 registers and its dQ kernels would not fit either, so those stay at one wave per SIMD.
   static constexpr bool PAIR2_TWO = !F32 && NPAIR == 2 && DK <= 64 && DV <= 64;
-  static constexpr int FW_NW = TWO ? NW2 : PAIR2_TWO ? 8 : 4, FW_QW = 1, FW_BN = F32 ? 32 : 64;
-  static constexpr int FW_WPE = TWO || PAIR2_TWO ? 2 : 1;
+  static constexpr bool FW2 = PAIR2_TWO || (!F32 && POLY == POLY_SP);
+  static constexpr int FW_NW = TWO ? NW2 : FW2 ? 8 : 4, FW_QW = 1, FW_BN = F32 ? 32 : 64;
+  static constexpr int FW_WPE = TWO || FW2 ? 2 : 1;
   static constexpr int BQ_NW = TWO ? NW2 : PAIR2_TWO ? 8 : 4, BQ_QW = 1, BQ_BN = F32 ? 32 : 64;
   static constexpr int BQ_WPE = TWO || PAIR2_TWO ? 2 : 1;
   static constexpr bool KV_SPLIT = TWO;  // separate dV and dK passes at two waves per SIMD
@@ -164,9 +167,10 @@ k_fwd(const KParams p) {
   typedef Tile<T, BN, DKP> KTile;
   typedef Tile<T, BN, DVP> VTile;
   constexpr int BUF = NPAIR * KTile::BYTES + VTile::BYTES;
-  // three tile buffers for the pipelined unmasked run when they fit the 160 KB of LDS, else two
+  // three tile buffers for the pipelined unmasked run when they fit the 160 KB of LDS, else two (and two for the
+  // two-wave signed_product forward above head dim 64, whose pipeline registers would not fit)
   constexpr bool CHUNKED = Stage<T, BN, DK, DKP, NT>::TOTAL % NT == 0 && Stage<T, BN, DV, DVP, NT>::TOTAL % NT == 0;
-  constexpr int NBUF = CHUNKED && NKB >= 2 && 3 * BUF <= 160 * 1024 ? 3 : 2;
+  constexpr int NBUF = CHUNKED && NKB >= 2 && 3 * BUF <= 160 * 1024 && !(POLY == POLY_SP && (DK > 64 || DV > 64)) ? 3 : 2;
   // The block's Q rows come in, and its O rows go out, through LDS as whole coalesced rows (ROWLDS; not with
   // zero-padded head dims, whose pad columns in the tile buffers must stay zero).
   typedef Tile<T, BM, DKP> QTile;
