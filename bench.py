@@ -84,15 +84,15 @@ def time_events(fn, reps):
 
 def kernel_times(kind, q, k, q2, k2, v, do, doc, rs, degree, reps):
     """Average duration (ms) of each launch of the fwd, dV, dK and dQ kernels (one dK/dV kernel for the two-pair
-    kinds; plus the dO pre-scaling pass when the operator uses it), timed with HIP events on the stream the library
-    launches on (torch's current stream)."""
+    kinds and for head dims up to 64; plus the dO pre-scaling pass when the operator uses it), timed with HIP events
+    on the stream the library launches on (torch's current stream)."""
     import torch
     from tensor_train_ing_amd import _abi
     from tensor_train_ing_amd.poly_attn import _desc, _problem, _stream, doc_bounds
     lib = _abi.load()
     K = KIND_CODES[kind]
     two = kind in TWO_PAIR_KINDS
-    H = q.shape[1]
+    H, D = q.shape[1], q.shape[-1]
     coef = torch.tensor([[0.1, 0.2, -0.3, 1.0]], device=q.device).repeat(H, 1) if kind == "lower_degree_mix" else None
     b = torch.full((H,), 0.5, device=q.device) if kind == "offset_square" else None
     dstart, qend = doc_bounds(doc)
@@ -116,7 +116,9 @@ def kernel_times(kind, q, k, q2, k2, v, do, doc, rs, degree, reps):
     fwd = lambda: _abi.check(lib.tnpa_forward(ctypes.byref(prob), ctypes.byref(od), st), "fwd")  # noqa: E731
     out = {}
     scale = [("bwd_scale", phase(_abi.PHASE_KV_SCALE, "scale"))] if dos is not None else []
-    if two:  # one dK/dV kernel (it writes the scaled dO itself when given the workspace)
+    # the key side is one dK/dV kernel for the two-pair kinds and for head dims up to 64 (it writes the scaled dO
+    # itself when given the workspace), separate dV and dK passes otherwise
+    if two or D <= 64:
         kv = [("bwd_kv", phase(_abi.PHASE_KV, "kv"))]
         scale = []
     else:
@@ -254,7 +256,9 @@ def main(argv=None):
     # matmul units each kernel executes: fwd QK^T + PV; dV pass S + dV; dK pass S + dP + dK; dQ pass S + dP + dQ;
     # two pairs: fwd S1 + S2 + PV, dK/dV kernel S1 + S2 + dP + dV + dK1 + dK2, dQ S1 + S2 + dP + dQ1 + dQ2 (the
     # row-scaling pass, when used, is a bandwidth kernel with no matrix work)
-    units = {"fwd": 3, "bwd_kv": 6, "bwd_q": 5} if two else {"fwd": 2, "bwd_dv": 2, "bwd_dk": 3, "bwd_q": 3}
+    # (one pair, head dims up to 64: one dK/dV kernel, S + dP + dV + dK)
+    units = ({"fwd": 3, "bwd_kv": 6, "bwd_q": 5} if two else {"fwd": 2, "bwd_kv": 4, "bwd_q": 3} if D <= 64
+             else {"fwd": 2, "bwd_dv": 2, "bwd_dk": 3, "bwd_q": 3})
     dom = max(units, key=lambda n: kt[n])
     ach = units[dom] * unit / (kt[dom] * 1e-3) / 1e12
     line = {

@@ -112,7 +112,8 @@ int tnpa_backward(const tnpa_problem_t* problem, const tnpa_grads_t* grads, void
  * tnlm/kernels/poly_attn.py:298-299,304-306); TNPA_PHASE_Q writes dq1, (dq2) (ref _bwd_q, :302-303). The passes
  * read only inputs, so they may run on different streams concurrently. Gradients a phase does not write may be
  * left NULL. tnpa_backward(...) == tnpa_backward_phase(..., TNPA_PHASE_KV | TNPA_PHASE_Q, ...).
- * For 16-bit inputs with one q/k pair the key side is itself three launches, selectable instead of TNPA_PHASE_KV:
+ * For 16-bit inputs with one q/k pair and a head dim above 64 the key side is itself three launches, selectable
+ * instead of TNPA_PHASE_KV:
  * TNPA_PHASE_KV_SCALE writes dout_scaled (required), TNPA_PHASE_KV_DV writes dv, TNPA_PHASE_KV_DK writes dk1 and
  * dpar; the dV and dK passes read dout_scaled as already written when its data is not NULL, and scale dout
  * themselves otherwise. Other configurations run dK and dV in one kernel and accept only the two together

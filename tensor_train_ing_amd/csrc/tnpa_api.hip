@@ -386,7 +386,7 @@ int tnpa_backward_phase(const tnpa_problem_t* problem, const tnpa_grads_t* grads
     return fail(TNPA_ERR_INVALID, "TNPA_PHASE_KV already includes the TNPA_PHASE_KV_* parts");
   const tnpa_problem_t& p = *problem;
   const int es = esize(p.dtype);
-  const bool split = tnpa::kv_split(p.dtype == TNPA_F32, poly_of(p));
+  const bool split = tnpa::kv_split(p.dtype == TNPA_F32, poly_of(p), p.head_dim_k, p.head_dim_v);
   const int kvsel = (phases & TNPA_PHASE_KV) ? 3 : ((phases & TNPA_PHASE_KV_DV) ? 1 : 0) | ((phases & TNPA_PHASE_KV_DK) ? 2 : 0);
   if (!split && (kvsel == 1 || kvsel == 2))
     return fail(TNPA_ERR_UNSUPPORTED, "this configuration computes dK and dV in one kernel: ask for both passes");

@@ -147,8 +147,10 @@ template <typename T, int POLY, int DK, int DV> struct Cfg {
   static constexpr int FW_WPE = TWO || FW2 ? 2 : 1;
   static constexpr int BQ_NW = TWO ? NW2 : PAIR2_TWO ? 8 : 4, BQ_QW = 1, BQ_BN = F32 ? 32 : 64;
   static constexpr int BQ_WPE = TWO || PAIR2_TWO ? 2 : 1;
-  static constexpr bool KV_SPLIT = TWO;  // separate dV and dK passes at two waves per SIMD
-  static constexpr int KV_NW = KV_SPLIT ? NW2 : 4, KV_KW = 1, KV_BM = F32 ? 32 : 64, KV_WPE = 1;
+  // Key side: separate dV and dK passes at two waves per SIMD for head dim 128 (one kernel holding dK, dV, K and V
+  // would need 376 registers there); up to 64 the combined kernel fits 256 registers and saves the S recompute.
+  static constexpr bool KV_SPLIT = TWO && !SMALL;
+  static constexpr int KV_NW = KV_SPLIT ? NW2 : 4, KV_KW = 1, KV_BM = F32 ? 32 : 64, KV_WPE = SMALL ? 2 : 1;
   static constexpr int KV_KEYS = KV_NW * KV_KW * 32;
 };
 
@@ -1255,7 +1257,7 @@ template <typename T, int POLY, int DK, int DV> hipError_t launch_fwd(const KPar
 
 template <typename T, int POLY, int DK, int DV> hipError_t launch_bwd_kv(const KParams& p, hipStream_t st) {
   typedef Cfg<T, POLY, DK, DV> C;
-  static_assert(C::KV_KEYS == (C::KV_SPLIT && !C::SMALL ? 256 : 128), "dK/dV block size mirrors kv_block_keys()");
+  static_assert(C::KV_KEYS == (C::KV_SPLIT ? 256 : 128), "dK/dV block size mirrors kv_block_keys()");
   const int grid = p.B * p.H * ((p.T + C::KV_KEYS - 1) / C::KV_KEYS);
   if constexpr (C::KV_SPLIT) {
     if (p.kvsel & 1)

@@ -39,14 +39,15 @@ struct KParams {
   float gf;  // factor on dQ and dK (p*sm^p, sm^2 or sm)
 };
 
-// Whether the key side runs as separate dV and dK passes (16-bit inputs, one q/k pair); mirrors Cfg::KV_SPLIT.
-inline bool kv_split(bool f32, int poly) { return !f32 && !two_pair_poly(poly); }
+// Whether the key side runs as separate dV and dK passes (16-bit inputs, one q/k pair, a head dim above 64);
+// mirrors Cfg::KV_SPLIT.
+inline bool kv_split(bool f32, int poly, int dk, int dv) {
+  return !f32 && !two_pair_poly(poly) && (dk > 64 || dv > 64);
+}
 
 // Keys per dK/dV workgroup (sizes the dcoef/db partials); mirrors Cfg::KV_KEYS: eight waves of 32 keys for the split
-// passes (two waves per SIMD) with head dims above 64, four waves otherwise.
-inline int kv_block_keys(bool f32, int poly, int dk, int dv) {
-  return kv_split(f32, poly) && (dk > 64 || dv > 64) ? 256 : 128;
-}
+// passes, four waves for the combined kernel.
+inline int kv_block_keys(bool f32, int poly, int dk, int dv) { return kv_split(f32, poly, dk, dv) ? 256 : 128; }
 
 // Whether the dK/dV passes scale dO by the row scale themselves at no cost: they stage the dO rows a step ahead and
 // apply the factor when writing them to LDS (three-buffer staging; 16-bit inputs, one q/k pair, and 64-row tiles
