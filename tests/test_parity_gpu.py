@@ -253,6 +253,27 @@ def test_d128_offset_square(T):
     _check(compare(res, ref), BF16_FRO, BF16_MAX)
 
 
+# ------------------------------------------------------------------ 16-bit, head dims up to 64
+# One q/k pair: four-wave blocks of 128 rows, two per CU, and one combined dK/dV kernel (4 matrix products);
+# two pairs: eight-wave forward and dQ at two waves per SIMD. Documents, padding, odd lengths, mixed dk/dv.
+@pytest.mark.parametrize("kind", ["power", "offset_square", "signed_product", "lower_degree_mix"])
+@pytest.mark.parametrize("dk,dv", [(64, 64), (32, 32), (64, 32), (32, 64), (16, 64)])
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_small_head_dims_16bit(kind, dk, dv, dtype):
+    B, H, T = 2, 3, 333
+    print(f"[small head dims] kind={kind} dk={dk} dv={dv} dtype={dtype} B{B} H{H} T{T}", flush=True)
+    res, ref = _case(kind, B, H, T, dk, dv, dtype, docs=_doc_rows(B, T), degree=2 if kind == "power" else None,
+                     qk_scale=dk ** -0.25, seed=dk + dv)
+    _check(compare(res, ref), BF16_FRO, BF16_MAX)
+
+
+@pytest.mark.parametrize("B,H,T", [(1, 8, 1000), (3, 1, 850), (2, 5, 129)])
+def test_small_head_dim_block_counts(B, H, T):
+    """Odd and even numbers of 128-row blocks at head dim 64, B*H a multiple of 8 and not."""
+    res, ref = _case("power", B, H, T, 64, 64, torch.bfloat16, docs=_doc_rows(B, T), degree=2, qk_scale=64 ** -0.25)
+    _check(compare(res, ref), BF16_FRO, BF16_MAX)
+
+
 def test_d128_bthd_layout():
     """(B, T, H, d) storage, the model's layout: time stride H*d, read in place."""
     res, ref = _case("power", 2, 4, 200, 128, 128, torch.bfloat16, docs=_doc_rows(2, 200), degree=2,
