@@ -150,7 +150,10 @@ template <typename T, int POLY, int DK, int DV> struct Cfg {
   // Key side: separate dV and dK passes at two waves per SIMD for head dim 128 (one kernel holding dK, dV, K and V
   // would need 376 registers there); up to 64 the combined kernel fits 256 registers and saves the S recompute.
   static constexpr bool KV_SPLIT = TWO && !SMALL;
-  static constexpr int KV_NW = KV_SPLIT ? NW2 : 4, KV_KW = 1, KV_BM = F32 ? 32 : 64, KV_WPE = SMALL ? 2 : 1;
+  // (two pairs at head dim 128: 32-query tiles, whose operand reads the compiler keeps in flight fit the one-wave
+  // kernel's 512 registers without spills; 64-query tiles spilled 13 registers and ran 20% slower)
+  static constexpr int KV_NW = KV_SPLIT ? NW2 : 4, KV_KW = 1, KV_BM = F32 || (NPAIR == 2 && DK > 64) ? 32 : 64;
+  static constexpr int KV_WPE = SMALL ? 2 : 1;
   static constexpr int KV_KEYS = KV_NW * KV_KW * 32;
 };
 
