@@ -143,7 +143,9 @@ template <typename T, int POLY, int DK, int DV> struct Cfg {
   // spill 315 registers and its dQ kernels would not fit either, so those stay at one wave per SIMD.
   static constexpr bool PAIR2_TWO = !F32 && NPAIR == 2 && DK <= 64 && DV <= 64;
   static constexpr bool FW2 = PAIR2_TWO || (!F32 && POLY == POLY_SP);
-  static constexpr int FW_NW = TWO ? NW2 : FW2 ? 8 : 4, FW_QW = 1, FW_BN = F32 ? 32 : 64;
+  // (the two-pair forward up to head dim 64 in four-wave workgroups, two per CU with two staging buffers each: 10%
+  // faster than one eight-wave workgroup; the two-pair dQ kernel measured no better that way)
+  static constexpr int FW_NW = TWO ? NW2 : PAIR2_TWO ? 4 : FW2 ? 8 : 4, FW_QW = 1, FW_BN = F32 ? 32 : 64;
   static constexpr int FW_WPE = TWO || FW2 ? 2 : 1;
   static constexpr int BQ_NW = TWO ? NW2 : PAIR2_TWO ? 8 : 4, BQ_QW = 1, BQ_BN = F32 ? 32 : 64;
   static constexpr int BQ_WPE = TWO || PAIR2_TWO ? 2 : 1;
@@ -162,6 +164,8 @@ template <typename T, int POLY, int DK, int DV> struct Cfg {
 template <typename T, int POLY, int DK, int DV, int NW, int QW, int BN, int WPE>
 __global__ void __attribute__((amdgpu_flat_work_group_size(NW * 64, NW * 64), amdgpu_waves_per_eu(WPE)))
 k_fwd(const KParams p) {
+  // four-wave workgroups at two waves per SIMD share a CU in pairs: each gets half of the 160 KB of LDS
+  constexpr int LDS_CAP = NW == 4 && WPE == 2 ? 80 * 1024 : 160 * 1024;
   typedef Mfma<T> M;
   typedef typename M::Op Op;
   constexpr int KC = M::KC, EPL = M::EPL, NT = NW * 64;
@@ -175,14 +179,14 @@ k_fwd(const KParams p) {
   // three tile buffers for the pipelined unmasked run when they fit the 160 KB of LDS, else two (and two for the
   // two-wave signed_product forward above head dim 64, whose pipeline registers would not fit)
   constexpr bool CHUNKED = Stage<T, BN, DK, DKP, NT>::TOTAL % NT == 0 && Stage<T, BN, DV, DVP, NT>::TOTAL % NT == 0;
-  constexpr int NBUF = CHUNKED && NKB >= 2 && 3 * BUF <= 160 * 1024 && !(POLY == POLY_SP && (DK > 64 || DV > 64)) ? 3 : 2;
+  constexpr int NBUF = CHUNKED && NKB >= 2 && 3 * BUF <= LDS_CAP && !(POLY == POLY_SP && (DK > 64 || DV > 64)) ? 3 : 2;
   // The block's Q rows come in, and its O rows go out, through LDS as whole coalesced rows (ROWLDS; not with
   // zero-padded head dims, whose pad columns in the tile buffers must stay zero).
   typedef Tile<T, BM, DKP> QTile;
   typedef Tile<T, BM, DVP> OTile;
-  constexpr bool ROWLDS = DKP == DK && DVP == DV && NPAIR * QTile::BYTES <= 160 * 1024;
+  constexpr bool ROWLDS = DKP == DK && DVP == DV && NPAIR * QTile::BYTES <= LDS_CAP;
   constexpr int SMEM = cmax(NBUF * BUF, cmax(ROWLDS ? NPAIR * QTile::BYTES : 0, OTile::BYTES));
-  static_assert(SMEM <= 160 * 1024, "LDS");
+  static_assert(SMEM <= LDS_CAP, "LDS");
   __shared__ __attribute__((aligned(16))) char smem_[SMEM];
   char TNPA_LDS* smem = (char TNPA_LDS*)smem_;
 
@@ -565,6 +569,8 @@ k_fwd(const KParams p) {
 template <typename T, int POLY, int DK, int DV, int NW, int QW, int BN, int WPE>
 __global__ void __attribute__((amdgpu_flat_work_group_size(NW * 64, NW * 64), amdgpu_waves_per_eu(WPE)))
 k_bwd_q(const KParams p) {
+  // four-wave workgroups at two waves per SIMD share a CU in pairs: each gets half of the 160 KB of LDS
+  constexpr int LDS_CAP = NW == 4 && WPE == 2 ? 80 * 1024 : 160 * 1024;
   typedef Mfma<T> M;
   typedef typename M::Op Op;
   constexpr int KC = M::KC, EPL = M::EPL, NT = NW * 64;
@@ -578,14 +584,14 @@ k_bwd_q(const KParams p) {
   typedef PartStager<T, BN, DK, DKP, DV, DVP, NT, NPAIR> Stager;
   // three tile buffers (each tile staged over two steps, its parts in different sub-blocks) when they fit the
   // 160 KB of LDS and the tile splits evenly over the threads, else two
-  constexpr int NBUF = Stager::OK && NKB >= 2 && 3 * BUF <= 160 * 1024 ? 3 : 2;
+  constexpr int NBUF = Stager::OK && NKB >= 2 && 3 * BUF <= LDS_CAP ? 3 : 2;
   // The block's Q and dO rows come in, and its dQ rows go out, through LDS as whole coalesced rows (ROWLDS; not
   // with zero-padded head dims, whose pad columns in the tile buffers must stay zero).
   typedef Tile<T, BM, DKP> QTile;
   typedef Tile<T, BM, DVP> DOTile;
-  constexpr bool ROWLDS = DKP == DK && DVP == DV && NPAIR * QTile::BYTES + DOTile::BYTES <= 160 * 1024;
+  constexpr bool ROWLDS = DKP == DK && DVP == DV && NPAIR * QTile::BYTES + DOTile::BYTES <= LDS_CAP;
   constexpr int SMEM = cmax(NBUF * BUF, cmax(ROWLDS ? NPAIR * QTile::BYTES + DOTile::BYTES : 0, QTile::BYTES));
-  static_assert(SMEM <= 160 * 1024, "LDS");
+  static_assert(SMEM <= LDS_CAP, "LDS");
   __shared__ __attribute__((aligned(16))) char smem_[SMEM];
   char TNPA_LDS* smem = (char TNPA_LDS*)smem_;
 
