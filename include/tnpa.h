@@ -68,9 +68,10 @@ typedef struct {
  * (column 0 = db for offset_square, the 4 columns = dcoef for lower_degree_mix); both may be NULL for
  * signed_product / power, and are required for the other two kinds.
  * dout_scaled is an optional caller-allocated workspace (B,H,T,dv) in the problem dtype: when its data is not NULL
- * the dK/dV pass first writes row_scale[b,t] * dout[b,h,t,:] into it (computed in fp32, rounded to the dtype,
- * exactly as the pass would round it on the fly) and then streams it instead of rescaling dout per tile. It has no
- * counterpart in the reference (whose Triton kernel scales in registers). */
+ * the dK/dV pass first writes row_scale[b,t] * dout[b,h,t,:] into it (computed in fp32, rounded to the dtype) and
+ * then streams it instead of applying the row scale itself (per staged dO tile with two staging buffers, exactly
+ * the same product and rounding; to P and H in fp32 with three, as the reference does). It has no counterpart in
+ * the reference (whose Triton kernel scales in registers). */
 typedef struct {
   tnpa_tensor_t dout, dq1, dk1, dq2, dk2, dv;
   float* dpar_partial;
@@ -98,8 +99,8 @@ int tnpa_forward(const tnpa_problem_t* problem, const tnpa_tensor_t* out, void* 
 /* Floats of dpar_partial workspace tnpa_backward needs for this problem (0 for signed_product / power). */
 int64_t tnpa_dpar_workspace_floats(const tnpa_problem_t* problem);
 
-/* 1 if passing tnpa_grads_t.dout_scaled makes tnpa_backward faster for this problem, 0 if the dK/dV passes scale
- * dout as cheaply themselves (16-bit inputs, one q/k pair, head dims multiples of 64) or the problem is NULL. No
+/* 1 if passing tnpa_grads_t.dout_scaled makes tnpa_backward faster for this problem, 0 if the dK/dV passes apply
+ * the row scale as cheaply themselves (16-bit inputs, one q/k pair, three staging buffers) or the problem is NULL. No
  * counterpart in the reference (a sizing query like tnpa_dpar_workspace_floats). */
 int32_t tnpa_dout_scaled_helps(const tnpa_problem_t* problem);
 

@@ -272,8 +272,6 @@ template <typename T, int ROWS, int DA, int DAP, int DB, int DBP, int NT, int NA
   const T* pb;
   int64_t sta[NA], stb;
   int T_;
-  const float* bscale = nullptr;  // optional per-row factor applied to the B rows when they are written to LDS
-  float fb[SB::PER];
 
   __device__ inline void init(const T* const* a, const int64_t* ast, const T* b, int64_t bst, int nrows) {
 #pragma unroll
@@ -298,10 +296,6 @@ template <typename T, int ROWS, int DA, int DAP, int DB, int DBP, int NT, int NA
     } else {
       const int k = q - NA * SA::PER;
       sb.load_buf(k, rows_rsrc<T>(pb, stb, n1, T_, DB), ob[k]);
-      if (bscale != nullptr) {
-        const int row = n1 + ((int)threadIdx.x + k * NT) / SB::NCHG;
-        fb[k] = row < T_ ? bscale[row] : 0.f;
-      }
     }
   }
   __device__ inline void store_part(int q, char TNPA_LDS* buf) const {
@@ -310,22 +304,7 @@ template <typename T, int ROWS, int DA, int DAP, int DB, int DBP, int NT, int NA
       sa[i].store_raw(k, buf + i * TA::BYTES);
     } else {
       const int k = q - NA * SA::PER;
-      if (bscale == nullptr) {
-        sb.store_raw(k, buf + NA * TA::BYTES);
-      } else {  // same product and rounding as Stage::load_scaled
-        SB t;
-        t.r[k] = sb.r[k];
-        if constexpr (sizeof(T) == 2) {
-          T* e = reinterpret_cast<T*>(&t.r[k]);
-#pragma unroll
-          for (int j = 0; j < 8; ++j) e[j] = (T)((float)e[j] * fb[k]);
-        } else {
-          float* e = reinterpret_cast<float*>(&t.r[k]);
-#pragma unroll
-          for (int j = 0; j < 4; ++j) e[j] *= fb[k];
-        }
-        t.store_raw(k, buf + NA * TA::BYTES);
-      }
+      sb.store_raw(k, buf + NA * TA::BYTES);
     }
   }
   // rows n1 .. n1 + ROWS - 1 into registers / registers into an LDS buffer: part 1 = the A tiles, 2 = the B tile

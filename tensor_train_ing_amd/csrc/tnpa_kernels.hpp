@@ -871,7 +871,8 @@ k_bwd_kv(const KParams p) {
   constexpr int BNK = NW * KW * 32;
   typedef Tile<T, BMQ, DKP> QTile;
   typedef Tile<T, BMQ, DVP> OTile;
-  constexpr int BUF = NPAIR * QTile::BYTES + OTile::BYTES + BMQ * 4;
+  // per buffer: the q tiles, the dO tile, the tile's document starts (int) and row scales (float)
+  constexpr int BUF = NPAIR * QTile::BYTES + OTile::BYTES + BMQ * 8;
   typedef PartStager<T, BMQ, DK, DKP, DV, DVP, NT, NPAIR> Stager;
   // three tile buffers (each query tile staged over two steps, one chunk per thread at a time) when they fit the
   // 160 KB of LDS and the tile splits evenly over the threads, else two (and for the two-pair kinds, whose single
@@ -970,23 +971,34 @@ k_bwd_kv(const KParams p) {
   constexpr int DSOFF = NPAIR * QTile::BYTES + OTile::BYTES;
   const T* dscp = head_ptr<T>(p.dsc, b, hd);
   auto ds_of = [&](const int m) { return m + (int)threadIdx.x < T_ ? dst[m + threadIdx.x] : INT_MAX; };
+  // Three buffers: the row scale multiplies P and H in fp32 (as ref: tnlm/kernels/poly_attn.py:119-122 does), read
+  // per query from LDS next to the document starts; 1 when the caller's dO is already scaled. Two buffers: dO is
+  // scaled (by the caller, or here while staging) instead.
+  auto sc_of = [&](const int m) {
+    return p.dpre ? 1.0f : (m + (int)threadIdx.x < T_ ? rsc[m + threadIdx.x] : 0.f);
+  };
   int dsv = 0;
+  float scv = 0.f;
   Stager stg;
   if constexpr (NBUF == 3) {
-    // dO' rows: pre-scaled by the caller, or scaled here when written to LDS
-    if (p.dpre) {
-      stg.init(qp, qst, dscp, p.dsc.st, T_);
-    } else {
-      stg.init(qp, qst, dop, p.dout.st, T_);
-      stg.bscale = rsc;
-    }
+    if (p.dpre) stg.init(qp, qst, dscp, p.dsc.st, T_);
+    else stg.init(qp, qst, dop, p.dout.st, T_);
     stg.load(3, qlo);
-    if (threadIdx.x < BMQ) dsv = ds_of(qlo);
+    if (threadIdx.x < BMQ) {
+      dsv = ds_of(qlo);
+      scv = sc_of(qlo);
+    }
 #pragma unroll
     for (int q = 0; q < Stager::NPARTS; ++q) stg.store_part(q, smem);
-    if (threadIdx.x < BMQ) ((int TNPA_LDS*)(smem + DSOFF))[threadIdx.x] = dsv;
+    if (threadIdx.x < BMQ) {
+      ((int TNPA_LDS*)(smem + DSOFF))[threadIdx.x] = dsv;
+      ((float TNPA_LDS*)(smem + DSOFF + BMQ * 4))[threadIdx.x] = scv;
+    }
     stg.load(3, qlo + BMQ);
-    if (threadIdx.x < BMQ) dsv = ds_of(qlo + BMQ);
+    if (threadIdx.x < BMQ) {
+      dsv = ds_of(qlo + BMQ);
+      scv = sc_of(qlo + BMQ);
+    }
   } else {
 #pragma unroll
     for (int pr = 0; pr < NPAIR; ++pr) sq[pr].load(qp[pr], qst[pr], qlo, T_ - qlo);
@@ -1040,12 +1052,18 @@ k_bwd_kv(const KParams p) {
     for (int s = 0; s < KW; ++s) {
       if (!(ALL || ((am >> s) & 1u))) continue;
       float pv[16], d1[16], d2[16];
+      // row scale of each accumulator row (query): from LDS with three-buffer staging, else 1 (dO came scaled)
+      float rsr[16];
+#pragma unroll
+      for (int r = 0; r < 16; ++r)
+        rsr[r] = NBUF == 3 ? ((const float TNPA_LDS*)(dsl + BMQ))[32 * qb + key_off<T>(r, h)] : 1.0f;
       if (FULL || ((fm >> s) & 1u)) {
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
           const float r1 = sacc[0][s][r], r2 = sacc[NPAIR - 1][s][r];
-          if constexpr (WANT_DV) pv[r] = poly_value<POLY, MODE == KV_BOTH>(r1, r2, p.kind, p.deg, p.sm, cf);
-          if constexpr (WANT_DK) poly_grad<POLY, PAR, MODE == KV_BOTH>(r1, r2, pacc[s][r], p.kind, p.deg, p.sm, cf, d1[r], d2[r], gsum);
+          if constexpr (WANT_DV) pv[r] = poly_value<POLY, MODE == KV_BOTH>(r1, r2, p.kind, p.deg, p.sm, cf) * rsr[r];
+          if constexpr (WANT_DK)
+            poly_grad<POLY, PAR, MODE == KV_BOTH>(r1, r2, pacc[s][r] * rsr[r], p.kind, p.deg, p.sm, cf, d1[r], d2[r], gsum);
         }
       } else {
         const int key = ka[s] + l32;
@@ -1054,9 +1072,10 @@ k_bwd_kv(const KParams p) {
           const int qo = 32 * qb + key_off<T>(r, h);
           const bool vis = key <= m + qo && dsl[qo] <= key;
           const float r1 = sacc[0][s][r], r2 = sacc[NPAIR - 1][s][r];
-          if constexpr (WANT_DV) pv[r] = vis ? poly_value<POLY, MODE == KV_BOTH>(r1, r2, p.kind, p.deg, p.sm, cf) : 0.f;
+          if constexpr (WANT_DV)
+            pv[r] = vis ? poly_value<POLY, MODE == KV_BOTH>(r1, r2, p.kind, p.deg, p.sm, cf) * rsr[r] : 0.f;
           if constexpr (WANT_DK)
-            poly_grad<POLY, PAR, MODE == KV_BOTH>(r1, r2, vis ? pacc[s][r] : 0.f, p.kind, p.deg, p.sm, cf, d1[r], d2[r], gsum);
+            poly_grad<POLY, PAR, MODE == KV_BOTH>(r1, r2, vis ? pacc[s][r] * rsr[r] : 0.f, p.kind, p.deg, p.sm, cf, d1[r], d2[r], gsum);
         }
       }
 #pragma unroll
@@ -1111,7 +1130,9 @@ k_bwd_kv(const KParams p) {
           }
         if (point == 0 && threadIdx.x < BMQ) {
           ((int TNPA_LDS*)(b1 + DSOFF))[threadIdx.x] = dsv;
+          ((float TNPA_LDS*)(b1 + DSOFF + BMQ * 4))[threadIdx.x] = scv;
           dsv = ds_of(m + 2 * BMQ);
+          scv = sc_of(m + 2 * BMQ);
         }
       }
     };

@@ -284,8 +284,11 @@ def test_d128_bthd_layout():
 @pytest.mark.parametrize("kind,dtype", [("power", torch.bfloat16), ("offset_square", torch.float16),
                                         ("lower_degree_mix", torch.bfloat16), ("power", torch.float32)])
 def test_prescaled_dout_matches_in_pass_scaling(kind, dtype):
-    """The dK/dV pass streaming the library-written row_scale * dO workspace gives bit-identical gradients to the
-    pass that scales dO while staging it (both round the product to the input dtype)."""
+    """The dK/dV pass streaming the library-written row_scale * dO workspace against the pass without it. fp32 and
+    the two-pair kinds scale dO while staging it without the workspace: the same product and rounding, so
+    bit-identical gradients. 16-bit one-pair kinds at head dim 128 apply the row scale to P and H in fp32 instead (as
+    the reference does), which rounds differently: equal within 5e-3 (relative Frobenius), both within the bf16
+    tolerance of the float64 reference."""
     import ctypes
     from tensor_train_ing_amd import _abi
     from tensor_train_ing_amd.poly_attn import KINDS, _desc, _problem, _stream, doc_bounds
@@ -315,9 +318,23 @@ def test_prescaled_dout_matches_in_pass_scaling(kind, dtype):
                    "kv")
         torch.cuda.synchronize()
         outs.append((dk1, dv, dk2 if two else None, dpar if kind in ("offset_square", "lower_degree_mix") else None))
-    for a, b2 in zip(*outs):
-        if a is not None:
+    ph_scaling = dtype != torch.float32 and not two  # the in-pass path scales P and H (three-buffer staging)
+    if ph_scaling:
+        ref = dense_reference(kind, q1, k1, q2, k2, v, dout, docs, rs, coef, bb, 2 if kind == "power" else None)
+        names = ("dk1", "dv", None, "db" if kind == "offset_square" else None)
+    for i, (a, b2) in enumerate(zip(*outs)):
+        if a is None:
+            continue
+        if not ph_scaling:
             assert torch.equal(a, b2)
+            continue
+        assert rel_fro(a, b2) < 5e-3, (i, rel_fro(a, b2))
+        name = names[i]
+        if name == "db":
+            a, b2 = a[:, 0], b2[:, 0]
+        if name is not None:
+            for x in (a, b2):
+                assert rel_fro(x, ref[name]) < BF16_FRO and rel_max(x, ref[name]) < BF16_MAX, name
 
 
 @pytest.mark.parametrize("kind", ["power", "offset_square"])
