@@ -89,3 +89,17 @@ def test_bench_counts_exactly_the_visible_pairs(T, L):
     from oracle import visible_mask
     doc = (np.arange(T) // L if L else np.zeros(T, dtype=np.int64))[None].astype(np.int64)
     assert bench.npairs(T, L) == int(visible_mask(doc).sum())
+
+
+def test_bench_refuses_more_than_one_gpu(capsys):
+    """This build measures one GPU: --gpus N > 1 exits with status 2 and says why (no torch or GPU touched)."""
+    import bench
+    assert bench.main(["--gpus", "2"]) == 2
+    assert "one GPU" in capsys.readouterr().err
+
+
+def test_bench_cpu_baseline_runs_on_a_small_sample():
+    """The CPU-baseline leg (the oracle timed on host cores) on a tiny workload: a positive rate and its sample."""
+    import bench
+    r = bench.cpu_baseline(1, 2, 64, 16, 2, 0.5)
+    assert r["value"] > 0 and r["kind"] == "port" and r["cores"] >= 1 and "slices" in r["sample"]
