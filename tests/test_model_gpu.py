@@ -36,12 +36,13 @@ def _pair(kind, mlp, dev, degree=2):
     return ref, hip
 
 
-@pytest.mark.parametrize("kind,mlp", [("signed_product", "bilinear"), ("offset_square", "bilinear"),
-                                      ("lower_degree_mix", "affine_bilinear"), ("power", "bilinear")])
-def test_model_hip_backend_matches_reference(kind, mlp):
+@pytest.mark.parametrize("kind,mlp,degree", [("signed_product", "bilinear", 2), ("offset_square", "bilinear", 2),
+                                             ("lower_degree_mix", "affine_bilinear", 2), ("power", "bilinear", 2),
+                                             ("power", "bilinear", 4)])
+def test_model_hip_backend_matches_reference(kind, mlp, degree):
     dev = torch.device("cuda:0")
-    print(f"[model parity] kind={kind} mlp={mlp} B2 T100 fp32", flush=True)
-    ref, hip = _pair(kind, mlp, dev)
+    print(f"[model parity] kind={kind} mlp={mlp} degree={degree} B2 T100 fp32", flush=True)
+    ref, hip = _pair(kind, mlp, dev, degree)
     idx, doc, tgt = _batch(dev)
     _, lr = ref(idx, doc, tgt)
     lr.backward()
@@ -54,7 +55,7 @@ def test_model_hip_backend_matches_reference(kind, mlp):
         assert _rel(b.grad, a.grad) < 1e-3, (n, _rel(b.grad, a.grad))
 
 
-@pytest.mark.parametrize("kind", ["signed_product", "offset_square", "power"])
+@pytest.mark.parametrize("kind", ["signed_product", "offset_square", "lower_degree_mix", "power"])
 def test_compiled_model_matches_eager(kind):
     """torch.compile(fullgraph=True) traces the model with the operator as opaque tnpa:: custom ops (a graph break
     would raise); loss and gradients equal the eager run's."""
