@@ -1,18 +1,25 @@
 """Benchmark: causal polynomial attention fwd+bwd TFLOP/s on one MI355X (BASELINE.json headline).
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--config 1b] [--kind power] [--cpu-seconds S]
-                    [--no-cpu-baseline]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--config 1b] [--kind power] [--dtype bf16]
+                    [--doc-len L] [--cpu-seconds S] [--no-cpu-baseline]
 
 A step is one forward + backward of the polynomial attention operator (default kind "power" at the config's
-degree; degree 2 equals the reference's signed_product with shared pairs) over one batch of seeded synthetic bf16
-inputs resident in HBM: q, k ~ N(0,1)/D^(1/4), v, dO ~ N(0,1), one causal document per row, row scale
-(t+1)^-1/2. --kind signed_product / lower_degree_mix draw a second q/k pair the same way (the reference model's
-default kind); those lines count 11 matmul units per step instead of 7 and carry no CPU baseline.
+degree; degree 2 equals the reference's signed_product with shared pairs) over one batch of seeded synthetic inputs
+resident in HBM: q, k ~ N(0,1)/D^(1/4), v, dO ~ N(0,1), one causal document per row, row scale (t+1)^-1/2.
+--kind signed_product / lower_degree_mix draw a second q/k pair the same way (the reference model's default kind);
+those lines count 11 matmul units per step instead of 7. --dtype f32 runs the fp32 path (the reference's "ieee"
+precision) against the fp32 MFMA peak.
+
+Timing: W untimed steps, then K steps with a HIP event recorded on the launch stream (torch's current stream)
+between consecutive steps; ms_per_step is the K-step total over K (the whole-job rate), ms_per_step_median the
+median of the K intervals. Each kernel of the step is then timed alone (median of --kernel-reps launches, an event
+pair around each), and the forward alone likewise (fwd_ms_median).
 
 FLOP convention (exact causal pairs, power and mask not counted): Npairs = T(T+1)/2,
-fwd = 4*B*H*Npairs*D, fwd+bwd = 14*B*H*Npairs*D. Peak: MI355X dense bf16 MFMA, 2.5 PFLOP/s.
-Prints one JSON line (rank 0). The CPU baseline times the CPU oracle (oracle/, float32 numpy) on a bounded
-sample of (b, h) slices of the same workload.
+fwd = 4*B*H*Npairs*D, fwd+bwd = 14*B*H*Npairs*D. Peaks: MI355X dense bf16 MFMA 2.5 PFLOP/s, fp32 157.3 TFLOP/s.
+Prints one JSON line (rank 0). The CPU baseline times the dense restatement of the reference attention in float32
+torch (oracle/torch_dense.py; backward by autograd) on the host's cores, on a bounded sample of (b, h) slices of
+the same inputs.
 """
 from __future__ import annotations
 
@@ -20,10 +27,12 @@ import argparse
 import ctypes
 import json
 import os
+import statistics
+import subprocess
 import sys
 import time
 
-PEAK_TFLOPS = 2500.0  # MI355X dense bf16 MFMA
+PEAKS = {"bf16": 2500.0, "f32": 157.3}  # MI355X dense MFMA, TFLOP/s
 METRIC = "poly-attn fwd+bwd TFLOP/s at B8 H16 T2048 D128 bf16; % of MI355X MFMA peak"
 
 KIND_CODES = {"signed_product": 0, "offset_square": 1, "lower_degree_mix": 2, "power": 3}
@@ -34,6 +43,11 @@ CONFIGS = {  # name: (B, H, T, D, degree, boost_rows, seed) -- BASELINE.json con
     "p4": (4, 16, 2048, 128, 4, 0.01, 3),
     "7b": (2, 32, 4096, 128, 2, 0.0, 4),
 }
+# matrix units (of 2*B*H*Npairs*D FLOP) each launch executes: fwd QK^T + PV; dv pass S + dV; dk pass S + dP + dK;
+# combined key side S + dP + dV + dK; dq pass S + dP + dQ; with two pairs one more S, dK and dQ each. The dO
+# row-scaling pass and the dpar reduction are bandwidth kernels with no matrix work.
+UNITS_ONE = {"fwd": 2, "dv": 2, "dk": 3, "kv": 4, "q": 3, "scale": 0, "dpar": 0}
+UNITS_TWO = {"fwd": 3, "kv": 6, "q": 5, "scale": 0, "dpar": 0}
 
 
 def npairs(T, doc_len=0):
@@ -44,10 +58,11 @@ def npairs(T, doc_len=0):
     return full * doc_len * (doc_len + 1) // 2 + rest * (rest + 1) // 2
 
 
-def make_inputs(B, H, T, D, boost, seed, device, two_pairs=False, doc_len=0):
-    """Seeded CPU draws cast to bf16 on the CPU: q, k (and q2, k2 for the two-pair kinds, drawn after dO so the
-    one-pair inputs do not change), v, dO; one document per row; row scale (t+1)^-1/2."""
+def make_inputs(B, H, T, D, boost, seed, device, two_pairs=False, doc_len=0, dtype=None):
+    """Seeded CPU draws cast to the dtype (bf16 by default) on the CPU: q, k (and q2, k2 for the two-pair kinds,
+    drawn after dO so the one-pair inputs do not change), v, dO; one document per row; row scale (t+1)^-1/2."""
     import torch
+    dtype = dtype or torch.bfloat16
     g = torch.Generator().manual_seed(seed)
     mk = lambda s: (torch.randn(B, H, T, D, generator=g) * s)  # noqa: E731
     q, k = mk(D ** -0.25), mk(D ** -0.25)
@@ -57,7 +72,7 @@ def make_inputs(B, H, T, D, boost, seed, device, two_pairs=False, doc_len=0):
             x.mul_(torch.where(rows, 4.0, 1.0)[:, None, :, None])
     v, do = mk(1.0), mk(1.0)
     q2, k2 = (mk(D ** -0.25), mk(D ** -0.25)) if two_pairs else (None, None)
-    cast = lambda x: None if x is None else x.to(torch.bfloat16).to(device)  # noqa: E731
+    cast = lambda x: None if x is None else x.to(dtype).to(device)  # noqa: E731
     q, k, v, do, q2, k2 = (cast(x) for x in (q, k, v, do, q2, k2))
     if doc_len:  # contiguous documents of doc_len tokens; row scale (position in document + 1)^-1/2
         t = torch.arange(T, device=device)
@@ -71,28 +86,47 @@ def make_inputs(B, H, T, D, boost, seed, device, two_pairs=False, doc_len=0):
     return q, k, v, do, doc, rs
 
 
-def time_events(fn, reps):
+def event_intervals(fn, reps):
+    """Runs fn reps times back to back with a HIP event between consecutive runs on the current stream; returns
+    the reps intervals (ms)."""
     import torch
-    s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    s.record()
-    for _ in range(reps):
+    evs = [torch.cuda.Event(enable_timing=True) for _ in range(reps + 1)]
+    evs[0].record()
+    for i in range(reps):
         fn()
-    e.record()
-    e.synchronize()
-    return s.elapsed_time(e) / reps
+        evs[i + 1].record()
+    evs[-1].synchronize()
+    return [evs[i].elapsed_time(evs[i + 1]) for i in range(reps)]
+
+
+def median_each(fn, reps):
+    """Median duration (ms) of fn over reps runs, each bracketed by its own event pair (after 3 untimed runs)."""
+    import torch
+    for _ in range(3):
+        fn()
+    torch.cuda.synchronize()
+    times = []
+    s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    for _ in range(reps):
+        s.record()
+        fn()
+        e.record()
+        e.synchronize()
+        times.append(s.elapsed_time(e))
+    return statistics.median(times)
 
 
 def kernel_times(kind, q, k, q2, k2, v, do, doc, rs, degree, reps):
-    """Average duration (ms) of each launch of the fwd, dV, dK and dQ kernels (one dK/dV kernel for the two-pair
-    kinds and for head dims up to 64; plus the dO pre-scaling pass when the operator uses it), timed with HIP events
-    on the stream the library launches on (torch's current stream)."""
+    """Median duration (ms) of each launch of the step, timed alone with HIP events on the stream the library
+    launches on (torch's current stream): the forward, then each launch of the backward plan in order (the
+    library's internal launch-level entry point; a launch run alone reads what the earlier ones wrote)."""
     import torch
     from tensor_train_ing_amd import _abi
     from tensor_train_ing_amd.poly_attn import _desc, _problem, _stream, doc_bounds
     lib = _abi.load()
     K = KIND_CODES[kind]
     two = kind in TWO_PAIR_KINDS
-    H, D = q.shape[1], q.shape[-1]
+    H = q.shape[1]
     coef = torch.tensor([[0.1, 0.2, -0.3, 1.0]], device=q.device).repeat(H, 1) if kind == "lower_degree_mix" else None
     b = torch.full((H,), 0.5, device=q.device) if kind == "offset_square" else None
     dstart, qend = doc_bounds(doc)
@@ -101,34 +135,20 @@ def kernel_times(kind, q, k, q2, k2, v, do, doc, rs, degree, reps):
     o = torch.empty_like(v)
     dq, dk, dv = torch.empty_like(q), torch.empty_like(k), torch.empty_like(v)
     dq2, dk2 = (torch.empty_like(q), torch.empty_like(k)) if two else (dq, dk)
-    par = kind in ("offset_square", "lower_degree_mix")
-    ws = torch.empty(max(1, lib.tnpa_dpar_workspace_floats(ctypes.byref(prob))), device=q.device) if par else None
-    dpar = torch.empty(H, 4, device=q.device) if par else None
-    # the row-scaled dO workspace, passed exactly when the operator passes it
-    dos = torch.empty_like(do) if lib.tnpa_dout_scaled_helps(ctypes.byref(prob)) else None
-    grads = _abi.Grads(_desc(do), _desc(dq), _desc(dk), _desc(dq2), _desc(dk2), _desc(dv),
-                       ws.data_ptr() if par else None, dpar.data_ptr() if par else None,
-                       _desc(dos) if dos is not None else _abi.Tensor())
+    dpar = torch.empty(H, 4, device=q.device)
+    nbytes = lib.tnpa_backward_workspace_bytes(ctypes.byref(prob))
+    ws = torch.empty(max(nbytes, 256), dtype=torch.uint8, device=q.device)
+    grads = _abi.Grads(_desc(do), _desc(dq), _desc(dk), _desc(dq2), _desc(dk2), _desc(dv), dpar.data_ptr(),
+                       ws.data_ptr(), nbytes)
     st = _stream(q.device)
     od = _desc(o)
-    def phase(ph, name):
-        return lambda: _abi.check(lib.tnpa_backward_phase(ctypes.byref(prob), ctypes.byref(grads), ph, st), name)
-    fwd = lambda: _abi.check(lib.tnpa_forward(ctypes.byref(prob), ctypes.byref(od), st), "fwd")  # noqa: E731
-    out = {}
-    scale = [("bwd_scale", phase(_abi.PHASE_KV_SCALE, "scale"))] if dos is not None else []
-    # the key side is one dK/dV kernel for the two-pair kinds and for head dims up to 64 (it writes the scaled dO
-    # itself when given the workspace), separate dV and dK passes otherwise
-    if two or D <= 64:
-        kv = [("bwd_kv", phase(_abi.PHASE_KV, "kv"))]
-        scale = []
-    else:
-        kv = [("bwd_dv", phase(_abi.PHASE_KV_DV, "dv")), ("bwd_dk", phase(_abi.PHASE_KV_DK, "dk"))]
-    runs = [("fwd", fwd)] + scale + kv + [("bwd_q", phase(_abi.PHASE_Q, "q"))]
-    for name, fn in runs:
-        for _ in range(3):
-            fn()
-        torch.cuda.synchronize()
-        out[name] = time_events(fn, reps)
+    out = {"fwd": median_each(
+        lambda: _abi.check(lib.tnpa_forward(ctypes.byref(prob), ctypes.byref(od), st), "fwd"), reps)}
+    _abi.check(lib.tnpa_backward(ctypes.byref(prob), ctypes.byref(grads), st), "bwd")  # fills the workspace
+    for i in range(lib.tnpa_x_launches(ctypes.byref(prob), 0)):
+        name = lib.tnpa_x_launch_name(ctypes.byref(prob), 0, i).decode()
+        out[name] = median_each(
+            lambda: _abi.check(lib.tnpa_x_backward(ctypes.byref(prob), ctypes.byref(grads), 0, i, st), name), reps)
     return out
 
 
@@ -140,57 +160,90 @@ def measured_traffic(config, kernel):
         with open(path) as f:
             for line in f:
                 parts = line.split()
-                if len(parts) == 4 and parts[0] == "k_" + kernel:
+                if len(parts) == 4 and parts[0] == kernel:
                     return int(parts[3])
     except OSError:
         pass
     return None
 
 
-def cpu_baseline(B, H, T, D, degree, seconds):
-    """Times the CPU oracle (float32 numpy dense restatement) fwd+bwd over (b, h) slices until `seconds` pass."""
-    import numpy as np
-    sys.path.insert(0, os.path.dirname(os.path.abspath(__file__)))
-    from oracle import polynomial_attention, polynomial_attention_backward, row_scale_mask, visible_mask
+def cpu_model():
+    """The host CPU's model name (lscpu, else /proc/cpuinfo)."""
     try:
-        from threadpoolctl import threadpool_info
-        threads = max([i.get("num_threads", 1) for i in threadpool_info() if i.get("internal_api") == "openblas"]
-                      or [1])
-    except Exception:  # threadpoolctl missing: report the affinity size numpy's BLAS defaults to
-        threads = len(os.sched_getaffinity(0))
-    rng = np.random.default_rng(0)
-    C = row_scale_mask(visible_mask(np.zeros((1, T), dtype=np.int64)), 0.5, np.float32)
-    done, t0 = 0, time.perf_counter()
-    while done < B * H:
-        q, k = (rng.standard_normal((1, 1, T, D), dtype=np.float32) * D ** -0.25 for _ in range(2))
-        v, do = (rng.standard_normal((1, 1, T, D), dtype=np.float32) for _ in range(2))
-        polynomial_attention("power", q, k, None, None, v, C, degree=degree)
-        polynomial_attention_backward("power", q, k, None, None, v, C, do, degree=degree)
-        done += 1
-        if time.perf_counter() - t0 >= seconds:
+        out = subprocess.run(["lscpu"], capture_output=True, text=True, timeout=10).stdout
+        for line in out.splitlines():
+            if line.startswith("Model name:"):
+                return line.split(":", 1)[1].strip()
+    except (OSError, subprocess.SubprocessError):
+        pass
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def cpu_baseline(q, k, v, do, rs, degree, seconds):
+    """Times the dense restatement of the reference attention (oracle/torch_dense.py) in float32 torch on the host's
+    cores over (b, h) slices of the GPU run's own inputs (copied to the host and upcast), until `seconds` pass:
+    the forward alone, then forward + backward (autograd). Returns the cpu_baseline object."""
+    import torch
+    sys.path.insert(0, os.path.dirname(os.path.abspath(__file__)))
+    from oracle import causal_row_scale, dense_attention
+    threads = len(os.sched_getaffinity(0))
+    torch.set_num_threads(threads)
+    B, H, T, D = q.shape
+    slices = [(b, h) for b in range(B) for h in range(H)]
+    host = [x.detach().float().cpu() for x in (q, k, v, do)]
+    rsh = rs.detach().float().cpu()
+    fwd_t, step_t = [], []
+    t0 = time.perf_counter()
+    for b, h in slices:
+        qs, ks, vs, ds = (x[b, h].contiguous() for x in host)
+        C = causal_row_scale(rsh[b])
+        t1 = time.perf_counter()
+        with torch.no_grad():
+            dense_attention("power", qs, ks, None, None, vs, C, degree=degree)
+        t2 = time.perf_counter()
+        ins = [x.clone().requires_grad_() for x in (qs, ks, vs)]
+        y = dense_attention("power", ins[0], ins[1], None, None, ins[2], C, degree=degree)
+        torch.autograd.grad(y, ins, ds)
+        t3 = time.perf_counter()
+        fwd_t.append(t2 - t1)
+        step_t.append(t3 - t2)
+        if t3 - t0 >= seconds:
             break
-    el = time.perf_counter() - t0
-    flops = 14.0 * done * npairs(T) * D
-    return {"value": round(flops / el / 1e12, 6), "unit": "TFLOP/s", "cores": int(threads), "kind": "port",
-            "sample": f"{done} of {B * H} (b,h) slices of the same workload, T={T} D={D}, fwd+bwd of the CPU oracle "
-                      f"(oracle/poly_attention.py, float32 numpy dense) in {el:.1f} s"}
+    n = len(step_t)
+    unit = 2.0 * npairs(T) * D  # one matrix unit of one (b, h) slice
+    fwd_med, step_med = statistics.median(fwd_t), statistics.median(step_t)
+    return {"value": round(7 * unit / step_med / 1e12, 6), "unit": "TFLOP/s", "cores": threads, "kind": "port",
+            "fwd_tflops": round(2 * unit / fwd_med / 1e12, 6),
+            "ms_per_slice_fwd": round(fwd_med * 1e3, 3), "ms_per_slice_fwd_bwd": round(step_med * 1e3, 3),
+            "cpu": cpu_model(), "threads": torch.get_num_threads(),
+            "sample": f"{n} of {B * H} (b,h) slices of the GPU run's inputs, T={T} D={D} degree {degree}: dense "
+                      f"float32 torch restatement of the reference attention (oracle/torch_dense.py), fwd alone and "
+                      f"fwd+bwd by autograd, median per slice, {threads} threads"}
 
 
 def main(argv=None):
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=30)
-    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--config", default="1b", choices=sorted(CONFIGS))
     ap.add_argument("--kind", default="power", choices=sorted(KIND_CODES),
                     help="polynomial family (default: power, the degree-p kind BASELINE.json's configs name; "
                          "signed_product with distinct q2/k2 is the reference model's default)")
+    ap.add_argument("--dtype", default="bf16", choices=sorted(PEAKS))
     ap.add_argument("--doc-len", type=int, default=0,
                     help="contiguous documents of this many tokens per row (0: one document; FLOPs count only the "
                          "visible pairs, so the rate shows how well invisible tiles are skipped)")
-    ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--cpu-seconds", type=float, default=15.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--kernel-reps", type=int, default=20)
+    ap.add_argument("--kernel-reps", type=int, default=50)
     ap.add_argument("--copy-probe-mib", type=int, default=0,
                     help="only run a plain device-to-device copy of this many MiB (3 times) and exit: the known-size "
                          "kernel that calibrates rocprofv3's FETCH_SIZE / WRITE_SIZE counters")
@@ -218,30 +271,34 @@ def main(argv=None):
     B, H, T, D, degree, boost, seed = CONFIGS[a.config]
     kind = a.kind
     two = kind in TWO_PAIR_KINDS
-    if two:
-        q, k, v, do, doc, rs, q2, k2 = make_inputs(B, H, T, D, boost, seed, dev, two_pairs=True, doc_len=a.doc_len)
-    else:
-        q, k, v, do, doc, rs = make_inputs(B, H, T, D, boost, seed, dev, doc_len=a.doc_len)
-        q2 = k2 = None
+    tdt = torch.bfloat16 if a.dtype == "bf16" else torch.float32
+    ins = make_inputs(B, H, T, D, boost, seed, dev, two_pairs=two, doc_len=a.doc_len, dtype=tdt)
+    q, k, v, do, doc, rs = ins[:6]
+    q2, k2 = (ins[6], ins[7]) if two else (None, None)
     coef = torch.tensor([[0.1, 0.2, -0.3, 1.0]], device=dev).repeat(H, 1) if kind == "lower_degree_mix" else None
     bias = torch.full((H,), 0.5, device=dev) if kind == "offset_square" else None
     leaves = [q, k] + ([q2, k2] if two else []) + [v]
     for x in leaves:
         x.requires_grad_()
+    deg = degree if kind == "power" else None
 
     def step():
-        out = poly_attention_hip(kind, q, k, q2, k2, v, doc, rs, coef=coef, b=bias,
-                                 degree=degree if kind == "power" else None)
+        out = poly_attention_hip(kind, q, k, q2, k2, v, doc, rs, coef=coef, b=bias, degree=deg)
         return torch.autograd.grad(out, leaves, do)
+
+    def fwd_only():
+        with torch.no_grad():
+            return poly_attention_hip(kind, q, k, q2, k2, v, doc, rs, coef=coef, b=bias, degree=deg)
 
     for _ in range(a.warmup):
         step()
     torch.cuda.synchronize()  # one process, one GPU: the synchronize is the whole barrier
     t0 = time.perf_counter()
-    ms_ev = time_events(step, a.steps)
+    iv = event_intervals(step, a.steps)
     torch.cuda.synchronize()
     wall_ms = (time.perf_counter() - t0) * 1e3 / a.steps
-    ms = max(ms_ev, 0.0)
+    ms = sum(iv) / len(iv)
+    fwd_iv = event_intervals(fwd_only, a.steps)
 
     # counted FLOPs (exact causal pairs): one q/k pair fwd 2 matmul units of 2*B*H*Npairs*D, fwd+bwd 7; two pairs
     # fwd 3 (S1, S2, PV), fwd+bwd 11
@@ -249,38 +306,37 @@ def main(argv=None):
     fl_fwd = (3 if two else 2) * unit
     fl_step = (11 if two else 7) * unit
     value = fl_step / (ms * 1e-3) / 1e12
+    peak = PEAKS[a.dtype]
 
     kt = kernel_times(kind, q.detach(), k.detach(), q2.detach() if two else None, k2.detach() if two else None,
                       v.detach(), do, doc, rs, degree, a.kernel_reps)
-    docs = f", documents of {a.doc_len} tokens" if a.doc_len else ", one document"
-    # matmul units each kernel executes: fwd QK^T + PV; dV pass S + dV; dK pass S + dP + dK; dQ pass S + dP + dQ;
-    # two pairs: fwd S1 + S2 + PV, dK/dV kernel S1 + S2 + dP + dV + dK1 + dK2, dQ S1 + S2 + dP + dQ1 + dQ2 (the
-    # row-scaling pass, when used, is a bandwidth kernel with no matrix work)
-    # (one pair, head dims up to 64: one dK/dV kernel, S + dP + dV + dK)
-    units = ({"fwd": 3, "bwd_kv": 6, "bwd_q": 5} if two else {"fwd": 2, "bwd_kv": 4, "bwd_q": 3} if D <= 64
-             else {"fwd": 2, "bwd_dv": 2, "bwd_dk": 3, "bwd_q": 3})
-    dom = max(units, key=lambda n: kt[n])
+    units = UNITS_TWO if two else UNITS_ONE
+    dom = max(kt, key=lambda n: kt[n])
     ach = units[dom] * unit / (kt[dom] * 1e-3) / 1e12
+    docs = f", documents of {a.doc_len} tokens" if a.doc_len else ", one document"
+    fwd_med = statistics.median(fwd_iv)
     line = {
         "metric": METRIC, "value": round(value, 2), "unit": "TFLOP/s", "n_gpus": 1, "steps": a.steps,
         "warmup": a.warmup, "ms_per_step": round(ms, 4), "higher_is_better": True, "scaling": "weak",
-        "vs_baseline": None, "dtype": "bf16", "data": "synthetic",
+        "vs_baseline": None, "dtype": a.dtype, "data": "synthetic",
         "config": {"workload": f"polynomial attention fwd+bwd, BASELINE config '{a.config}': B{B} H{H} T{T} D{D} "
                                + (f"degree {degree}" if kind == "power" else f"kind {kind}")
                                + f", causal{docs}, row scale (position in document + 1)^-1/2",
-                   "B": B, "H": H, "T": T, "D": D, "kind": kind, "degree": degree if kind == "power" else None,
-                   "doc_len": a.doc_len or T},
-        "pct_of_peak": round(100 * value / PEAK_TFLOPS, 2),
-        "fwd_tflops": round(fl_fwd / (kt["fwd"] * 1e-3) / 1e12, 2),
-        "fwd_pct_of_peak": round(100 * fl_fwd / (kt["fwd"] * 1e-3) / 1e12 / PEAK_TFLOPS, 2),
+                   "B": B, "H": H, "T": T, "D": D, "kind": kind, "degree": deg, "doc_len": a.doc_len or T},
+        "pct_of_peak": round(100 * value / peak, 2),
+        "ms_per_step_median": round(statistics.median(iv), 4),
+        "fwd_ms_median": round(fwd_med, 4),
+        "fwd_tflops": round(fl_fwd / (fwd_med * 1e-3) / 1e12, 2),
+        "fwd_pct_of_peak": round(100 * fl_fwd / (fwd_med * 1e-3) / 1e12 / peak, 2),
         "wall_ms_per_step": round(wall_ms, 4),
         "kernel_ms": {n: round(t, 4) for n, t in kt.items()},
-        "roofline": {"bound": "mfma", "kernel": dom, "achieved": round(ach, 2), "peak": PEAK_TFLOPS,
-                     "unit": "TFLOP/s", "frac": round(ach / PEAK_TFLOPS, 4),
-                     "traffic": measured_traffic(a.config, dom) if kind == "power" and not a.doc_len else None},
+        "roofline": {"bound": "mfma", "kernel": dom, "achieved": round(ach, 2), "peak": peak,
+                     "unit": "TFLOP/s", "frac": round(ach / peak, 4),
+                     "traffic": (measured_traffic(a.config, dom)
+                                 if kind == "power" and not a.doc_len and a.dtype == "bf16" else None)},
     }
     if not a.no_cpu_baseline and kind == "power" and not a.doc_len:
-        line["cpu_baseline"] = cpu_baseline(B, H, T, D, degree, a.cpu_seconds)
+        line["cpu_baseline"] = cpu_baseline(q, k, v, do, rs, degree, a.cpu_seconds)
     print(json.dumps(line), flush=True)
     return 0
 

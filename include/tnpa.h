@@ -24,7 +24,7 @@
 extern "C" {
 #endif
 
-#define TNPA_ABI_VERSION 2
+#define TNPA_ABI_VERSION 3
 
 typedef enum {
   TNPA_OK = 0,
@@ -63,20 +63,17 @@ typedef struct {
   const float* offset;
 } tnpa_problem_t;
 
-/* Gradients for tnpa_backward. dout is dL/dy (B,H,T,dv). dq2/dk2 are ignored for one-pair kinds. dpar_partial is
- * a caller-allocated fp32 workspace of tnpa_dpar_workspace_floats() floats, and dpar an (H,4) fp32 output
- * (column 0 = db for offset_square, the 4 columns = dcoef for lower_degree_mix); both may be NULL for
- * signed_product / power, and are required for the other two kinds.
- * dout_scaled is an optional caller-allocated workspace (B,H,T,dv) in the problem dtype: when its data is not NULL
- * the dK/dV pass first writes row_scale[b,t] * dout[b,h,t,:] into it (computed in fp32, rounded to the dtype) and
- * then streams it instead of applying the row scale itself (per staged dO tile with two staging buffers, exactly
- * the same product and rounding; to P and H in fp32 with three, as the reference does). It has no counterpart in
- * the reference (whose Triton kernel scales in registers). */
+/* Gradients for tnpa_backward. dout is dL/dy (B,H,T,dv). dq2/dk2 are ignored for one-pair kinds. dpar is an (H,4)
+ * fp32 output (column 0 = db for offset_square, the 4 columns = dcoef for lower_degree_mix), required for those two
+ * kinds and ignored otherwise. workspace is caller-allocated device memory of at least
+ * tnpa_backward_workspace_bytes(problem) bytes, 256-byte aligned (NULL when that is 0); its contents on entry do not
+ * matter and on return are unspecified. It stands for the reference's per-call scratch (the DPAR partials of
+ * ref: tnlm/kernels/poly_attn.py:296), so the library itself never allocates. */
 typedef struct {
   tnpa_tensor_t dout, dq1, dk1, dq2, dk2, dv;
-  float* dpar_partial;
   float* dpar;
-  tnpa_tensor_t dout_scaled;
+  void* workspace;
+  int64_t workspace_bytes;
 } tnpa_grads_t;
 
 /* Library ABI version (TNPA_ABI_VERSION). */
@@ -96,35 +93,15 @@ int tnpa_doc_bounds(const void* doc_ids, int32_t doc_is_int64, int64_t doc_strid
  * (PolyAttention.forward launch of _fwd). */
 int tnpa_forward(const tnpa_problem_t* problem, const tnpa_tensor_t* out, void* stream);
 
-/* Floats of dpar_partial workspace tnpa_backward needs for this problem (0 for signed_product / power). */
-int64_t tnpa_dpar_workspace_floats(const tnpa_problem_t* problem);
-
-/* 1 if passing tnpa_grads_t.dout_scaled makes tnpa_backward faster for this problem, 0 if the dK/dV passes apply
- * the row scale as cheaply themselves (16-bit inputs, one q/k pair, three staging buffers) or the problem is NULL. No
- * counterpart in the reference (a sizing query like tnpa_dpar_workspace_floats). */
-int32_t tnpa_dout_scaled_helps(const tnpa_problem_t* problem);
+/* Bytes of device workspace tnpa_backward needs for this problem (0 if none; -1 and tnpa_last_error() for an invalid
+ * problem). No counterpart in the reference, whose autograd function allocates its scratch itself
+ * (ref: tnlm/kernels/poly_attn.py:294-296); here the caller allocates it and passes tnpa_grads_t.workspace. */
+int64_t tnpa_backward_workspace_bytes(const tnpa_problem_t* problem);
 
 /* Backward: writes dq1, dk1, (dq2, dk2), dv, and dpar. Replaces ref: tnlm/kernels/poly_attn.py:286-309
  * (PolyAttention.backward: _bwd_kv, _bwd_q and the fixed-order dcoef/db reduction). Deterministic: no atomics,
- * every reduction in a fixed order. */
+ * every reduction in a fixed order. How the work is split into kernel launches is internal to the library. */
 int tnpa_backward(const tnpa_problem_t* problem, const tnpa_grads_t* grads, void* stream);
-
-/* The passes of tnpa_backward, selectable: TNPA_PHASE_KV writes dk1, (dk2), dv and dpar (ref _bwd_kv,
- * tnlm/kernels/poly_attn.py:298-299,304-306); TNPA_PHASE_Q writes dq1, (dq2) (ref _bwd_q, :302-303). The passes
- * read only inputs, so they may run on different streams concurrently. Gradients a phase does not write may be
- * left NULL. tnpa_backward(...) == tnpa_backward_phase(..., TNPA_PHASE_KV | TNPA_PHASE_Q, ...).
- * For 16-bit inputs with one q/k pair and a head dim above 64 the key side is itself three launches, selectable
- * instead of TNPA_PHASE_KV:
- * TNPA_PHASE_KV_SCALE writes dout_scaled (required), TNPA_PHASE_KV_DV writes dv, TNPA_PHASE_KV_DK writes dk1 and
- * dpar; the dV and dK passes read dout_scaled as already written when its data is not NULL, and scale dout
- * themselves otherwise. Other configurations run dK and dV in one kernel and accept only the two together
- * (TNPA_ERR_UNSUPPORTED otherwise). */
-#define TNPA_PHASE_KV 1
-#define TNPA_PHASE_Q 2
-#define TNPA_PHASE_KV_SCALE 4
-#define TNPA_PHASE_KV_DV 8
-#define TNPA_PHASE_KV_DK 16
-int tnpa_backward_phase(const tnpa_problem_t* problem, const tnpa_grads_t* grads, int32_t phases, void* stream);
 
 #ifdef __cplusplus
 }

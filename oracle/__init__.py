@@ -18,3 +18,4 @@ from .poly_attention import (  # noqa: F401
     scores,
     visible_mask,
 )
+from .torch_dense import causal_row_scale, dense_attention  # noqa: F401

@@ -1,4 +1,5 @@
-"""ctypes bindings for libtnpa.so (declared in include/tnpa.h).
+"""ctypes bindings for libtnpa.so: the public C ABI (include/tnpa.h) and the internal launch-level entry points
+(csrc/tnpa_internal.h) that the benchmark and the tests use.
 
 The library must be built in-tree (``python -m tensor_train_ing_amd.build``); there is no fallback: loading fails
 loudly when the shared library is missing.
@@ -10,7 +11,7 @@ import os
 from pathlib import Path
 
 LIB_PATH = Path(__file__).resolve().parent / "libtnpa.so"
-ABI_VERSION = 2
+ABI_VERSION = 3
 
 OK, ERR_INVALID, ERR_UNSUPPORTED, ERR_LAUNCH = 0, 1, 2, 3
 BF16, F32, F16 = 0, 1, 2
@@ -36,23 +37,29 @@ class Problem(ctypes.Structure):
 class Grads(ctypes.Structure):
     """tnpa_grads_t"""
     _fields_ = [("dout", Tensor), ("dq1", Tensor), ("dk1", Tensor), ("dq2", Tensor), ("dk2", Tensor),
-                ("dv", Tensor), ("dpar_partial", ctypes.c_void_p), ("dpar", ctypes.c_void_p),
-                ("dout_scaled", Tensor)]
+                ("dv", Tensor), ("dpar", ctypes.c_void_p), ("workspace", ctypes.c_void_p),
+                ("workspace_bytes", ctypes.c_int64)]
 
 
+# public ABI (include/tnpa.h)
 _SIGNATURES = {
     "tnpa_abi_version": (ctypes.c_int, []),
     "tnpa_last_error": (ctypes.c_char_p, []),
     "tnpa_doc_bounds": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_int32, ctypes.c_int64, ctypes.c_int32,
                                        ctypes.c_int32, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p]),
     "tnpa_forward": (ctypes.c_int, [ctypes.POINTER(Problem), ctypes.POINTER(Tensor), ctypes.c_void_p]),
-    "tnpa_dpar_workspace_floats": (ctypes.c_int64, [ctypes.POINTER(Problem)]),
-    "tnpa_dout_scaled_helps": (ctypes.c_int32, [ctypes.POINTER(Problem)]),
+    "tnpa_backward_workspace_bytes": (ctypes.c_int64, [ctypes.POINTER(Problem)]),
     "tnpa_backward": (ctypes.c_int, [ctypes.POINTER(Problem), ctypes.POINTER(Grads), ctypes.c_void_p]),
-    "tnpa_backward_phase": (ctypes.c_int, [ctypes.POINTER(Problem), ctypes.POINTER(Grads), ctypes.c_int32,
-                                           ctypes.c_void_p]),
 }
-PHASE_KV, PHASE_Q, PHASE_KV_SCALE, PHASE_KV_DV, PHASE_KV_DK = 1, 2, 4, 8, 16
+# internal entry points (csrc/tnpa_internal.h): the backward's launches one by one, and its plan options
+_INTERNAL = {
+    "tnpa_x_workspace_bytes": (ctypes.c_int64, [ctypes.POINTER(Problem), ctypes.c_int32]),
+    "tnpa_x_launches": (ctypes.c_int32, [ctypes.POINTER(Problem), ctypes.c_int32]),
+    "tnpa_x_launch_name": (ctypes.c_char_p, [ctypes.POINTER(Problem), ctypes.c_int32, ctypes.c_int32]),
+    "tnpa_x_backward": (ctypes.c_int, [ctypes.POINTER(Problem), ctypes.POINTER(Grads), ctypes.c_int32, ctypes.c_int32,
+                                       ctypes.c_void_p]),
+}
+X_PRESCALE_ON, X_PRESCALE_OFF = 1, 2
 
 _LIB = None
 
@@ -67,7 +74,7 @@ def load(path: os.PathLike | str | None = None) -> ctypes.CDLL:
         raise RuntimeError(f"{p} is missing: build the HIP library first (python -m tensor_train_ing_amd.build). "
                            "There is no CPU fallback for the HIP attention operator.")
     lib = ctypes.CDLL(str(p))
-    for name, (res, args) in _SIGNATURES.items():
+    for name, (res, args) in {**_SIGNATURES, **_INTERNAL}.items():
         fn = getattr(lib, name)
         fn.restype = res
         fn.argtypes = args

@@ -29,7 +29,7 @@ COMMON = [f"--offload-arch={ARCH}", "-O3", "-std=c++17", "-fPIC", "-Wall", "-Wno
 
 ELEMENT_TYPES = {"bf16": "__bf16", "f16": "_Float16", "f32": "float"}
 HEAD_DIMS = (16, 32, 64, 128)
-HEADERS = ("tnpa_device.hpp", "tnpa_kernels.hpp", "tnpa_params.hpp")
+HEADERS = ("tnpa_device.hpp", "tnpa_kernels.hpp", "tnpa_params.hpp", "tnpa_internal.h")
 
 
 def _units():

@@ -1,5 +1,6 @@
 // C ABI of libtnpa.so: argument validation, dtype/kind/head-dim dispatch to the kernel instantiations, the
-// document-bounds prepass and the fixed-order dcoef/db reduction.  Declared in include/tnpa.h.
+// document-bounds prepass, the backward plan (its launches and the carving of the caller's workspace) and the
+// fixed-order dcoef/db reduction. Declared in include/tnpa.h and tnpa_internal.h.
 #include <algorithm>
 #include <cmath>
 #include <cstdarg>
@@ -7,6 +8,7 @@
 #include <string>
 
 #include "../../include/tnpa.h"
+#include "tnpa_internal.h"
 #include "tnpa_params.hpp"
 
 namespace {
@@ -106,9 +108,18 @@ tnpa::KParams make_params(const tnpa_problem_t& p) {
   k.deg = p.kind == TNPA_POWER ? p.degree : 2;
   const double sm = 1.0 / std::sqrt((double)p.head_dim_k);
   k.sm = (float)sm;
+  // fp16: the kernels scale each score by sm before the polynomial (tnpa::prescaled), so only the chain-rule sm of
+  // dS/dr remains for the gradients
+  const bool pre = p.dtype == TNPA_F16;
   switch (p.kind) {
-    case TNPA_SIGNED_PRODUCT: k.vf = (float)(sm * sm); k.gf = (float)(sm * sm); break;
-    case TNPA_POWER: k.vf = (float)std::pow(sm, k.deg); k.gf = (float)(k.deg * std::pow(sm, k.deg)); break;
+    case TNPA_SIGNED_PRODUCT:
+      k.vf = pre ? 1.0f : (float)(sm * sm);
+      k.gf = pre ? (float)sm : (float)(sm * sm);
+      break;
+    case TNPA_POWER:
+      k.vf = pre ? 1.0f : (float)std::pow(sm, k.deg);
+      k.gf = pre ? (float)(k.deg * sm) : (float)(k.deg * std::pow(sm, k.deg));
+      break;
     default: k.vf = 1.0f; k.gf = (float)sm; break;
   }
   return k;
@@ -325,6 +336,124 @@ __global__ void k_dpar_reduce(const float* part, int B, int H, int NNB, float* o
   out[i] = acc;
 }
 
+// ---------------------------------------------------------------------------------------------- backward plan
+// The launches of one backward call and the carving of the caller's workspace:
+//   scale  row_scale * dO into the workspace (where the key side cannot scale dO for free, or when forced)
+//   kv     the combined dK/dV kernel, or dv and dk: the two passes of the split key side (16-bit, one q/k pair,
+//          head dim above 64)
+//   q      the dQ kernel
+//   dpar   the fixed-order dcoef/db reduction of the per-key-block partials (offset_square, lower_degree_mix)
+enum LaunchKind { L_SCALE = 0, L_KV = 1, L_DV = 2, L_DK = 3, L_Q = 4, L_DPAR = 5 };
+const char* const kLaunchNames[] = {"scale", "kv", "dv", "dk", "q", "dpar"};
+
+struct Plan {
+  int n = 0;
+  int what[6] = {0, 0, 0, 0, 0, 0};
+  bool prescale = false, par = false;
+  int nnb = 0;  // key blocks per row (dpar partials)
+  int64_t dpar_off = 0, dos_off = 0, bytes = 0;
+};
+
+int64_t align256(int64_t x) { return (x + 255) & ~(int64_t)255; }
+
+int make_plan(const tnpa_problem_t& p, int opts, Plan& pl) {
+  if ((opts & ~(TNPA_X_PRESCALE_ON | TNPA_X_PRESCALE_OFF)) != 0 ||
+      (opts & (TNPA_X_PRESCALE_ON | TNPA_X_PRESCALE_OFF)) == (TNPA_X_PRESCALE_ON | TNPA_X_PRESCALE_OFF))
+    return fail(TNPA_ERR_INVALID, "invalid backward options %d", opts);
+  const bool f32 = p.dtype == TNPA_F32;
+  const int poly = poly_of(p), dk = p.head_dim_k, dv = p.head_dim_v;
+  const bool split = tnpa::kv_split(f32, poly, dk, dv);
+  const bool helps = !tnpa::kv_scales_in_pass(f32, poly, dk, dv);
+  pl = Plan{};
+  pl.prescale = (opts & TNPA_X_PRESCALE_ON) ? true : (opts & TNPA_X_PRESCALE_OFF) ? false : helps;
+  pl.par = p.kind == TNPA_OFFSET_SQUARE || p.kind == TNPA_LOWER_DEGREE_MIX;
+  const int bk = tnpa::kv_block_keys(f32, poly, dk, dv);
+  pl.nnb = (p.seq_len + bk - 1) / bk;
+  const int64_t dpar_bytes = pl.par ? (int64_t)p.batch * p.heads * pl.nnb * 4 * (int64_t)sizeof(float) : 0;
+  const int64_t dos_bytes = pl.prescale ? (int64_t)p.batch * p.heads * p.seq_len * dv * esize(p.dtype) : 0;
+  pl.dpar_off = 0;
+  pl.dos_off = align256(dpar_bytes);
+  pl.bytes = pl.prescale ? pl.dos_off + align256(dos_bytes) : align256(dpar_bytes);
+  if (pl.prescale) pl.what[pl.n++] = L_SCALE;
+  if (split) {
+    pl.what[pl.n++] = L_DV;
+    pl.what[pl.n++] = L_DK;
+  } else {
+    pl.what[pl.n++] = L_KV;
+  }
+  pl.what[pl.n++] = L_Q;
+  if (pl.par) pl.what[pl.n++] = L_DPAR;
+  return TNPA_OK;
+}
+
+int run_backward(const tnpa_problem_t* problem, const tnpa_grads_t* grads, int opts, int only, hipStream_t stream) {
+  int rc = check_problem(problem);
+  if (rc) return rc;
+  if (grads == nullptr) return fail(TNPA_ERR_INVALID, "null grads");
+  const tnpa_problem_t& p = *problem;
+  Plan pl;
+  if ((rc = make_plan(p, opts, pl))) return rc;
+  if (only < -1 || only >= pl.n) return fail(TNPA_ERR_INVALID, "launch %d out of range (plan has %d)", only, pl.n);
+  if (grads->workspace_bytes < pl.bytes)
+    return fail(TNPA_ERR_INVALID, "workspace of %lld bytes, this problem needs %lld (tnpa_backward_workspace_bytes)",
+                (long long)grads->workspace_bytes, (long long)pl.bytes);
+  char* ws = (char*)grads->workspace;
+  if (pl.bytes > 0 && (ws == nullptr || ((uintptr_t)ws) % 256 != 0))
+    return fail(TNPA_ERR_INVALID, "workspace must be a non-null 256-byte aligned device pointer");
+  const int es = esize(p.dtype);
+  if ((rc = check_tensor(grads->dout, "dout", p, es))) return rc;
+  if ((rc = check_tensor(grads->dq1, "dq1", p, es))) return rc;
+  if ((rc = check_tensor(grads->dk1, "dk1", p, es))) return rc;
+  if ((rc = check_tensor(grads->dv, "dv", p, es))) return rc;
+  if (two_pairs(p.kind)) {
+    if ((rc = check_tensor(grads->dq2, "dq2", p, es))) return rc;
+    if ((rc = check_tensor(grads->dk2, "dk2", p, es))) return rc;
+  }
+  if (pl.par && grads->dpar == nullptr) return fail(TNPA_ERR_INVALID, "offset_square / lower_degree_mix need dpar (H,4)");
+  tnpa::KParams k = make_params(p);
+  k.dout = desc(grads->dout);
+  k.dq1 = desc(grads->dq1);
+  k.dk1 = desc(grads->dk1);
+  k.dq2 = two_pairs(p.kind) ? desc(grads->dq2) : desc(grads->dq1);
+  k.dk2 = two_pairs(p.kind) ? desc(grads->dk2) : desc(grads->dk1);
+  k.dv = desc(grads->dv);
+  k.dpar = pl.par ? (float*)(ws + pl.dpar_off) : nullptr;
+  tnpa_tensor_t dos{};
+  if (pl.prescale) {
+    const int64_t st = p.head_dim_v;
+    dos = tnpa_tensor_t{ws + pl.dos_off, (int64_t)p.heads * p.seq_len * st, (int64_t)p.seq_len * st, st};
+    k.dsc = desc(dos);
+    k.dpre = 1;
+  }
+  for (int i = 0; i < pl.n; ++i) {
+    if (only != -1 && i != only) continue;
+    hipError_t e = hipSuccess;
+    switch (pl.what[i]) {
+      case L_SCALE:
+        switch (p.dtype) {
+          case TNPA_BF16: e = scale_rows<__bf16>(p, grads->dout, dos, stream); break;
+          case TNPA_F16: e = scale_rows<_Float16>(p, grads->dout, dos, stream); break;
+          default: e = scale_rows<float>(p, grads->dout, dos, stream); break;
+        }
+        break;
+      case L_KV: k.kvsel = 3; e = run(PH_BWD_KV, p, k, stream); break;
+      case L_DV: k.kvsel = 1; e = run(PH_BWD_KV, p, k, stream); break;
+      case L_DK: k.kvsel = 2; e = run(PH_BWD_KV, p, k, stream); break;
+      case L_Q: e = run(PH_BWD_Q, p, k, stream); break;
+      case L_DPAR: {
+        const int n = p.heads * 4;
+        hipLaunchKernelGGL(k_dpar_reduce, dim3((n + 255) / 256), dim3(256), 0, stream, (const float*)k.dpar, p.batch,
+                           p.heads, pl.nnb, grads->dpar);
+        e = hipGetLastError();
+        break;
+      }
+    }
+    if (e != hipSuccess)
+      return fail(TNPA_ERR_LAUNCH, "tnpa_backward (%s): %s", kLaunchNames[pl.what[i]], hipGetErrorString(e));
+  }
+  return ok();
+}
+
 }  // namespace
 
 extern "C" {
@@ -359,106 +488,35 @@ int tnpa_forward(const tnpa_problem_t* problem, const tnpa_tensor_t* out, void* 
   return ok();
 }
 
-int64_t tnpa_dpar_workspace_floats(const tnpa_problem_t* problem) {
-  if (problem == nullptr) return 0;
-  if (problem->kind != TNPA_OFFSET_SQUARE && problem->kind != TNPA_LOWER_DEGREE_MIX) return 0;
-  const int bk = tnpa::kv_block_keys(problem->dtype == TNPA_F32, poly_of(*problem), problem->head_dim_k,
-                                     problem->head_dim_v);
-  const int64_t nnb = (problem->seq_len + bk - 1) / bk;
-  return (int64_t)problem->batch * problem->heads * nnb * 4;
-}
-
-int32_t tnpa_dout_scaled_helps(const tnpa_problem_t* problem) {
-  if (problem == nullptr) return 0;
-  return tnpa::kv_scales_in_pass(problem->dtype == TNPA_F32, poly_of(*problem), problem->head_dim_k,
-                                 problem->head_dim_v) ? 0 : 1;
-}
-
-int tnpa_backward_phase(const tnpa_problem_t* problem, const tnpa_grads_t* grads, int32_t phases, void* stream) {
-  int rc = check_problem(problem);
-  if (rc) return rc;
-  if (grads == nullptr) return fail(TNPA_ERR_INVALID, "null grads");
-  constexpr int ALL = TNPA_PHASE_KV | TNPA_PHASE_Q | TNPA_PHASE_KV_SCALE | TNPA_PHASE_KV_DV | TNPA_PHASE_KV_DK;
-  constexpr int KV_PARTS = TNPA_PHASE_KV_SCALE | TNPA_PHASE_KV_DV | TNPA_PHASE_KV_DK;
-  if (phases <= 0 || (phases & ~ALL) != 0)
-    return fail(TNPA_ERR_INVALID, "phases must be a nonzero combination of the TNPA_PHASE_* flags");
-  if ((phases & TNPA_PHASE_KV) && (phases & KV_PARTS))
-    return fail(TNPA_ERR_INVALID, "TNPA_PHASE_KV already includes the TNPA_PHASE_KV_* parts");
-  const tnpa_problem_t& p = *problem;
-  const int es = esize(p.dtype);
-  const bool split = tnpa::kv_split(p.dtype == TNPA_F32, poly_of(p), p.head_dim_k, p.head_dim_v);
-  const int kvsel = (phases & TNPA_PHASE_KV) ? 3 : ((phases & TNPA_PHASE_KV_DV) ? 1 : 0) | ((phases & TNPA_PHASE_KV_DK) ? 2 : 0);
-  if (!split && (kvsel == 1 || kvsel == 2))
-    return fail(TNPA_ERR_UNSUPPORTED, "this configuration computes dK and dV in one kernel: ask for both passes");
-  const bool scale_only = (phases & TNPA_PHASE_KV_SCALE) != 0;
-  if (scale_only && grads->dout_scaled.data == nullptr)
-    return fail(TNPA_ERR_INVALID, "TNPA_PHASE_KV_SCALE needs dout_scaled");
-  const bool kv = kvsel != 0, q = phases & TNPA_PHASE_Q;
-  const bool want_dv = kvsel & 1, want_dk = kvsel & 2;
-  if ((rc = check_tensor(grads->dout, "dout", p, es))) return rc;
-  if (q && (rc = check_tensor(grads->dq1, "dq1", p, es))) return rc;
-  if (want_dk && (rc = check_tensor(grads->dk1, "dk1", p, es))) return rc;
-  if (want_dv && (rc = check_tensor(grads->dv, "dv", p, es))) return rc;
-  if (two_pairs(p.kind)) {
-    if (q && (rc = check_tensor(grads->dq2, "dq2", p, es))) return rc;
-    if (want_dk && (rc = check_tensor(grads->dk2, "dk2", p, es))) return rc;
-  }
-  if (grads->dout_scaled.data != nullptr && (kv || scale_only) &&
-      (rc = check_tensor(grads->dout_scaled, "dout_scaled", p, es)))
-    return rc;
-  const bool par = want_dk && (p.kind == TNPA_OFFSET_SQUARE || p.kind == TNPA_LOWER_DEGREE_MIX);
-  if (par && (grads->dpar_partial == nullptr || grads->dpar == nullptr))
-    return fail(TNPA_ERR_INVALID, "offset_square / lower_degree_mix need dpar_partial and dpar");
-  tnpa::KParams k = make_params(p);
-  k.dout = desc(grads->dout);
-  if (q) {
-    k.dq1 = desc(grads->dq1);
-    k.dq2 = two_pairs(p.kind) ? desc(grads->dq2) : desc(grads->dq1);
-  }
-  if (want_dk) {
-    k.dk1 = desc(grads->dk1);
-    k.dk2 = two_pairs(p.kind) ? desc(grads->dk2) : desc(grads->dk1);
-  }
-  if (want_dv) k.dv = desc(grads->dv);
-  k.kvsel = kvsel;
-  k.dpar = par ? grads->dpar_partial : nullptr;
-  hipError_t e;
-  // the full key-side phase writes the scaled dO itself; the separate passes read what TNPA_PHASE_KV_SCALE wrote
-  const bool write_scaled = grads->dout_scaled.data != nullptr && ((phases & TNPA_PHASE_KV) || scale_only);
-  if (grads->dout_scaled.data != nullptr && kv) {
-    k.dsc = desc(grads->dout_scaled);
-    k.dpre = 1;
-  }
-  if (write_scaled) {
-    switch (p.dtype) {
-      case TNPA_BF16: e = scale_rows<__bf16>(p, grads->dout, grads->dout_scaled, (hipStream_t)stream); break;
-      case TNPA_F16: e = scale_rows<_Float16>(p, grads->dout, grads->dout_scaled, (hipStream_t)stream); break;
-      default: e = scale_rows<float>(p, grads->dout, grads->dout_scaled, (hipStream_t)stream); break;
-    }
-    if (e != hipSuccess) return fail(TNPA_ERR_LAUNCH, "tnpa_backward (row scaling): %s", hipGetErrorString(e));
-  }
-  if (kv) {
-    e = run(PH_BWD_KV, p, k, (hipStream_t)stream);
-    if (e != hipSuccess) return fail(TNPA_ERR_LAUNCH, "tnpa_backward (dK/dV): %s", hipGetErrorString(e));
-  }
-  if (q) {
-    e = run(PH_BWD_Q, p, k, (hipStream_t)stream);
-    if (e != hipSuccess) return fail(TNPA_ERR_LAUNCH, "tnpa_backward (dQ): %s", hipGetErrorString(e));
-  }
-  if (par) {
-    const int bk = tnpa::kv_block_keys(p.dtype == TNPA_F32, poly_of(p), p.head_dim_k, p.head_dim_v);
-    const int nnb = (p.seq_len + bk - 1) / bk;
-    const int n = p.heads * 4;
-    hipLaunchKernelGGL(k_dpar_reduce, dim3((n + 255) / 256), dim3(256), 0, (hipStream_t)stream, grads->dpar_partial,
-                       p.batch, p.heads, nnb, grads->dpar);
-    e = hipGetLastError();
-    if (e != hipSuccess) return fail(TNPA_ERR_LAUNCH, "tnpa_backward (dpar): %s", hipGetErrorString(e));
-  }
-  return ok();
-}
+int64_t tnpa_backward_workspace_bytes(const tnpa_problem_t* problem) { return tnpa_x_workspace_bytes(problem, 0); }
 
 int tnpa_backward(const tnpa_problem_t* problem, const tnpa_grads_t* grads, void* stream) {
-  return tnpa_backward_phase(problem, grads, TNPA_PHASE_KV | TNPA_PHASE_Q, stream);
+  return tnpa_x_backward(problem, grads, 0, -1, stream);
+}
+
+int64_t tnpa_x_workspace_bytes(const tnpa_problem_t* problem, int32_t opts) {
+  Plan pl;
+  if (check_problem(problem) || make_plan(*problem, opts, pl)) return -1;
+  ok();
+  return pl.bytes;
+}
+
+int32_t tnpa_x_launches(const tnpa_problem_t* problem, int32_t opts) {
+  Plan pl;
+  if (check_problem(problem) || make_plan(*problem, opts, pl)) return -1;
+  ok();
+  return pl.n;
+}
+
+const char* tnpa_x_launch_name(const tnpa_problem_t* problem, int32_t opts, int32_t i) {
+  Plan pl;
+  if (check_problem(problem) || make_plan(*problem, opts, pl) || i < 0 || i >= pl.n) return "";
+  return kLaunchNames[pl.what[i]];
+}
+
+int tnpa_x_backward(const tnpa_problem_t* problem, const tnpa_grads_t* grads, int32_t opts, int32_t only,
+                    void* stream) {
+  return run_backward(problem, grads, opts, only, (hipStream_t)stream);
 }
 
 }  // extern "C"

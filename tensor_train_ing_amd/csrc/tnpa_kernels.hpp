@@ -52,11 +52,25 @@ __device__ inline float upow(float x, int e) {
   return (e & 8) ? v * (x4 * x4) : v;
 }
 
-// A(S1, S2) on raw dot products r = q.k (homogeneous kinds fold sm^p into vf).  ref: tnlm/kernels/poly_attn.py:26-34
+// Whether the homogeneous families (power, signed_product) scale each raw score by sm before the polynomial, as
+// the reference does (ref: tnlm/kernels/poly_attn.py:63,66): for fp16, whose range is 65504, the unscaled r^p would
+// overflow where S^p does not (degree 4 at |q.k| > 16 with dk = 128). bf16 and fp32 keep fp32's range and fold sm^p
+// into vf / gf instead (rounding is scale-invariant there, so both placements give the same products).
+template <typename T, int POLY> __host__ __device__ constexpr bool prescaled() {
+  return sizeof(T) == 2 && !std::is_same<T, __bf16>::value &&
+         (POLY == POLY_POW2 || POLY == POLY_POW4 || POLY == POLY_GEN1 || POLY == POLY_SP);
+}
+
+// A(S1, S2) on raw dot products r = q.k (homogeneous kinds fold sm^p into vf unless PRE scales r by sm first).
+// ref: tnlm/kernels/poly_attn.py:26-34
 // KINDTEST (two-pair families only) keeps a never-taken test of the kind in the lower_degree_mix code: it changes
 // nothing in the results, but without it the one-wave dK/dV kernel of that kind needs 4x more scratch spills.
-template <int POLY, bool KINDTEST = false>
+template <int POLY, bool KINDTEST = false, bool PRE = false>
 __device__ inline float poly_value(float r1, float r2, int kind, int deg, float sm, const Coefs& c) {
+  if constexpr (PRE) {
+    r1 *= sm;
+    r2 *= sm;
+  }
   if constexpr (POLY == POLY_POW2) {
     return r1 * r1;
   } else if constexpr (POLY == POLY_POW4) {
@@ -78,9 +92,13 @@ __device__ inline float poly_value(float r1, float r2, int kind, int deg, float 
 
 // dS1, dS2 for a masked upstream H entry hg (gf carries the constant factors); optionally accumulates the
 // head-scalar partial sums g[0..3].  ref: tnlm/kernels/poly_attn.py:123-135,189-196
-template <int POLY, bool PAR, bool KINDTEST = false>
+template <int POLY, bool PAR, bool KINDTEST = false, bool PRE = false>
 __device__ inline void poly_grad(float r1, float r2, float hg, int kind, int deg, float sm, const Coefs& c,
                                  float& d1, float& d2, float* g) {
+  if constexpr (PRE) {
+    r1 *= sm;
+    r2 *= sm;
+  }
   if constexpr (POLY == POLY_POW2) {
     d1 = hg * r1;
     d2 = 0.f;
@@ -170,6 +188,7 @@ k_fwd(const KParams p) {
   typedef typename M::Op Op;
   constexpr int KC = M::KC, EPL = M::EPL, NT = NW * 64;
   constexpr int NPAIR = two_pair_poly(POLY) ? 2 : 1;
+  constexpr bool PRE = prescaled<T, POLY>();
   constexpr int DKP = DK < 32 ? 32 : DK, DVP = DV < 32 ? 32 : DV;
   constexpr int NCK = DK / KC, NDV = DVP / 32, NKB = BN / 32, NC2 = 32 / KC;
   constexpr int BM = NW * QW * 32;
@@ -294,13 +313,13 @@ k_fwd(const KParams p) {
       if (FULL || ((fm >> s) & 1u)) {
 #pragma unroll
         for (int r = 0; r < 16; ++r)
-          pv[r] = poly_value<POLY>(sacc[0][s][r], sacc[NPAIR - 1][s][r], p.kind, p.deg, p.sm, cf);
+          pv[r] = poly_value<POLY, false, PRE>(sacc[0][s][r], sacc[NPAIR - 1][s][r], p.kind, p.deg, p.sm, cf);
       } else {
         const int q = qa[s] + l32;
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
           const int key = key0 + key_off<T>(r, h);
-          const float val = poly_value<POLY>(sacc[0][s][r], sacc[NPAIR - 1][s][r], p.kind, p.deg, p.sm, cf);
+          const float val = poly_value<POLY, false, PRE>(sacc[0][s][r], sacc[NPAIR - 1][s][r], p.kind, p.deg, p.sm, cf);
           pv[r] = (key > q || key < dsq[s]) ? 0.f : val;
         }
       }
@@ -351,7 +370,7 @@ k_fwd(const KParams p) {
     for (int s = 0; s < QW; ++s) {
       float pv[16];
 #pragma unroll
-      for (int r = 0; r < 16; ++r) pv[r] = poly_value<POLY>(sacc[0][s][r], sacc[NPAIR - 1][s][r], p.kind, p.deg, p.sm, cf);
+      for (int r = 0; r < 16; ++r) pv[r] = poly_value<POLY, false, PRE>(sacc[0][s][r], sacc[NPAIR - 1][s][r], p.kind, p.deg, p.sm, cf);
 #pragma unroll
       for (int c2 = 0; c2 < NC2; ++c2) pop[s][c2] = M::cvt(pv + c2 * EPL);
     }
@@ -575,6 +594,7 @@ k_bwd_q(const KParams p) {
   typedef typename M::Op Op;
   constexpr int KC = M::KC, EPL = M::EPL, NT = NW * 64;
   constexpr int NPAIR = two_pair_poly(POLY) ? 2 : 1;
+  constexpr bool PRE = prescaled<T, POLY>();
   constexpr int DKP = DK < 32 ? 32 : DK, DVP = DV < 32 ? 32 : DV;
   constexpr int NCK = DK / KC, NCV = DV / KC, NDK = DKP / 32, NKB = BN / 32, NC2 = 32 / KC;
   constexpr int BM = NW * QW * 32;
@@ -723,6 +743,8 @@ k_bwd_q(const KParams p) {
         if (ALL || ((am >> s) & 1u)) pacc[s] = M::mma(a, dof[s][c], pacc[s]);
     }
     mid();
+    // H = row_scale * dO V^T before dS is formed and rounded, as ref: tnlm/kernels/poly_attn.py:188 does (keeps fp16
+    // dS in range where the unscaled H times S would not be)
     Op dso[NPAIR][QW][NC2];
 #pragma unroll
     for (int s = 0; s < QW; ++s) {
@@ -731,15 +753,15 @@ k_bwd_q(const KParams p) {
       if (FULL || ((fm >> s) & 1u)) {
 #pragma unroll
         for (int r = 0; r < 16; ++r)
-          poly_grad<POLY, false>(sacc[0][s][r], sacc[NPAIR - 1][s][r], pacc[s][r], p.kind, p.deg, p.sm, cf, d1[r],
+          poly_grad<POLY, false, false, PRE>(sacc[0][s][r], sacc[NPAIR - 1][s][r], pacc[s][r] * scq[s], p.kind, p.deg, p.sm, cf, d1[r],
                                  d2[r], nullptr);
       } else {
         const int q = qa[s] + l32;
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
           const int key = key0 + key_off<T>(r, h);
-          const float hg = (key > q || key < dsq[s]) ? 0.f : pacc[s][r];
-          poly_grad<POLY, false>(sacc[0][s][r], sacc[NPAIR - 1][s][r], hg, p.kind, p.deg, p.sm, cf, d1[r], d2[r],
+          const float hg = (key > q || key < dsq[s]) ? 0.f : pacc[s][r] * scq[s];
+          poly_grad<POLY, false, false, PRE>(sacc[0][s][r], sacc[NPAIR - 1][s][r], hg, p.kind, p.deg, p.sm, cf, d1[r], d2[r],
                                  nullptr);
         }
       }
@@ -837,14 +859,14 @@ k_bwd_q(const KParams p) {
   for (; j < j1; ++j) step(lo + j * BN, std::true_type{});
   for (; j < ntile; ++j) step(lo + j * BN, std::false_type{});
 
-  // dQ rows: scaled in registers, gathered in LDS, written as whole rows
+  // dQ rows: scaled by the chain-rule factor in registers, gathered in LDS, written as whole rows
   const TDesc* outs[2] = {&p.dq1, &p.dq2};
 #pragma unroll
   for (int pr = 0; pr < NPAIR; ++pr) {
     __syncthreads();  // every wave is done with the tile buffers (or with the previous pair's rows)
 #pragma unroll
     for (int s = 0; s < QW; ++s)
-      acc_rows_to_lds<T, QTile, NDK>(smem, 32 * (wave * QW + s), l32, h, dq[pr][s], scq[s] * p.gf, DK);
+      acc_rows_to_lds<T, QTile, NDK>(smem, 32 * (wave * QW + s), l32, h, dq[pr][s], p.gf, DK);
     __syncthreads();
     Stage<T, BM, DK, DKP, NT> os;
     os.copy_out(smem, head_ptr_w<T>(*outs[pr], b, hd), outs[pr]->st, m0, T_ - m0);
@@ -864,6 +886,7 @@ k_bwd_kv(const KParams p) {
   typedef typename M::Op Op;
   constexpr int KC = M::KC, EPL = M::EPL, NT = NW * 64;
   constexpr int NPAIR = two_pair_poly(POLY) ? 2 : 1;
+  constexpr bool PRE = prescaled<T, POLY>();
   constexpr bool PAR = (POLY == POLY_OS || POLY == POLY_GEN2) && MODE != KV_DV;  // kinds with head scalars
   constexpr bool WANT_DV = MODE != KV_DK, WANT_DK = MODE != KV_DV;
   constexpr int DKP = DK < 32 ? 32 : DK, DVP = DV < 32 ? 32 : DV;
@@ -1061,9 +1084,9 @@ k_bwd_kv(const KParams p) {
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
           const float r1 = sacc[0][s][r], r2 = sacc[NPAIR - 1][s][r];
-          if constexpr (WANT_DV) pv[r] = poly_value<POLY, MODE == KV_BOTH>(r1, r2, p.kind, p.deg, p.sm, cf) * rsr[r];
+          if constexpr (WANT_DV) pv[r] = poly_value<POLY, MODE == KV_BOTH, PRE>(r1, r2, p.kind, p.deg, p.sm, cf) * rsr[r];
           if constexpr (WANT_DK)
-            poly_grad<POLY, PAR, MODE == KV_BOTH>(r1, r2, pacc[s][r] * rsr[r], p.kind, p.deg, p.sm, cf, d1[r], d2[r], gsum);
+            poly_grad<POLY, PAR, MODE == KV_BOTH, PRE>(r1, r2, pacc[s][r] * rsr[r], p.kind, p.deg, p.sm, cf, d1[r], d2[r], gsum);
         }
       } else {
         const int key = ka[s] + l32;
@@ -1073,9 +1096,9 @@ k_bwd_kv(const KParams p) {
           const bool vis = key <= m + qo && dsl[qo] <= key;
           const float r1 = sacc[0][s][r], r2 = sacc[NPAIR - 1][s][r];
           if constexpr (WANT_DV)
-            pv[r] = vis ? poly_value<POLY, MODE == KV_BOTH>(r1, r2, p.kind, p.deg, p.sm, cf) * rsr[r] : 0.f;
+            pv[r] = vis ? poly_value<POLY, MODE == KV_BOTH, PRE>(r1, r2, p.kind, p.deg, p.sm, cf) * rsr[r] : 0.f;
           if constexpr (WANT_DK)
-            poly_grad<POLY, PAR, MODE == KV_BOTH>(r1, r2, vis ? pacc[s][r] * rsr[r] : 0.f, p.kind, p.deg, p.sm, cf, d1[r], d2[r], gsum);
+            poly_grad<POLY, PAR, MODE == KV_BOTH, PRE>(r1, r2, vis ? pacc[s][r] * rsr[r] : 0.f, p.kind, p.deg, p.sm, cf, d1[r], d2[r], gsum);
         }
       }
 #pragma unroll

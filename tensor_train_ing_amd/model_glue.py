@@ -29,21 +29,26 @@ def row_scales(doc_ids: torch.Tensor, positions: torch.Tensor, powers) -> dict:
 
 
 def fast_context(doc_ids: torch.Tensor, positions: torch.Tensor, powers, backend: str = "hip") -> dict:
-    """The fast-path part of the model context: doc ids, backend name and row scales (no visibility mask)."""
-    return {"doc_ids": doc_ids, "backend": backend, "row_scale": row_scales(doc_ids, positions, powers)}
+    """The fast-path part of the model context: doc ids, backend name, row scales (no visibility mask) and the
+    per-token document bounds, computed here once for every layer of the forward (one prepass launch per batch)."""
+    from .poly_attn import doc_bounds
+    return {"doc_ids": doc_ids, "backend": backend, "row_scale": row_scales(doc_ids, positions, powers),
+            "bounds": doc_bounds(doc_ids)}
 
 
 def attention(kind: str, q1, k1, q2, k2, v, ctx: dict, row_power: float, coef=None, b=None, degree=None):
     """Attention.forward's fast-path call (ref: tnlm/model.py:86-91) for ctx["backend"] == "hip": (B, H, T, dv)."""
     fn = poly_attention_for(ctx["backend"])
     kw = {"degree": degree} if kind == "power" else {}
-    return fn(kind, q1, k1, q2, k2, v, ctx["doc_ids"], ctx["row_scale"][row_power], coef=coef, b=b, **kw)
+    return fn(kind, q1, k1, q2, k2, v, ctx["doc_ids"], ctx["row_scale"][row_power], coef=coef, b=b,
+              bounds=ctx.get("bounds"), **kw)
 
 
 def source_files() -> list[Path]:
     """Every source file the operator is built from or runs: the Python package, the HIP kernels and the C ABI
     header (the built library is excluded)."""
-    files = sorted(PKG.rglob("*.py")) + sorted((PKG / "csrc").glob("*.hip")) + sorted((PKG / "csrc").glob("*.hpp"))
+    files = (sorted(PKG.rglob("*.py")) + sorted((PKG / "csrc").glob("*.hip")) + sorted((PKG / "csrc").glob("*.hpp"))
+             + sorted((PKG / "csrc").glob("*.h")))
     header = PKG.parent / "include" / "tnpa.h"
     if header.exists():
         files.append(header)

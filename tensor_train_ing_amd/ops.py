@@ -1,44 +1,54 @@
 """The polynomial attention as registered torch custom ops, for callers that compile their model.
 
 The reference trains a compiled model (ref: tnlm/train.py:353); its Triton operator is traced through. A ctypes
-call cannot be traced, so the same HIP kernels are registered here as two opaque custom ops with fake (shape)
+call cannot be traced, so the same HIP kernels are registered here as three opaque custom ops with fake (shape)
 implementations and an autograd formula:
 
-    tnpa::poly_attention           (kind, degree, q1, k1, q2?, k2?, v, doc_ids, row_scale, coef?, b?)
-                                   -> (o, doc_start, query_end)
+    tnpa::doc_bounds               (doc_ids) -> (doc_start, query_end)
+    tnpa::poly_attention           (kind, degree, q1, k1, q2?, k2?, v, doc_start, query_end, row_scale, coef?, b?) -> o
     tnpa::poly_attention_backward  (kind, degree, q1, k1, q2?, k2?, v, doc_start, query_end, row_scale, coef?, b?, dO)
                                    -> (dq1, dk1, dq2, dk2, dv, dpar)
 
 Outputs and gradients are contiguous (B, H, T, d); dq2/dk2 are empty for one-pair kinds and dpar is empty unless the
-kind has head parameters. The document bounds computed by the forward are handed to the backward, as the
-reference's autograd.Function saves its LO/HI (ref: tnlm/kernels/poly_attn.py:281).
-`poly_attention_hip` switches to these ops by itself while torch.compile traces it.
+kind has head parameters. The document bounds are an input of the attention op: computed once per batch by a model
+(or once per call when the caller passes none) and handed to the backward, as the reference's autograd.Function
+saves its LO/HI (ref: tnlm/kernels/poly_attn.py:281). `poly_attention_hip` switches to these ops by itself while
+torch.compile traces it.
 """
 from typing import Optional
 
 import torch
 
 from . import _abi
-from .poly_attn import _canonical, _prep, _run_backward, _run_forward
+from .poly_attn import _canonical, _prep, _run_backward, _run_forward, doc_bounds
 
 _PAR_KINDS = (_abi.OFFSET_SQUARE, _abi.LOWER_DEGREE_MIX)
 _TWO_PAIRS = (_abi.SIGNED_PRODUCT, _abi.LOWER_DEGREE_MIX)
 
 
+@torch.library.custom_op("tnpa::doc_bounds", mutates_args=())
+def doc_bounds_op(doc_ids: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
+    return doc_bounds(doc_ids)
+
+
+@doc_bounds_op.register_fake
+def _bounds_fake(doc_ids):
+    B, T = doc_ids.shape
+    return doc_ids.new_empty((B, T), dtype=torch.int32), doc_ids.new_empty((B, T), dtype=torch.int32)
+
+
 @torch.library.custom_op("tnpa::poly_attention", mutates_args=())
 def _fwd(kind: int, degree: int, q1: torch.Tensor, k1: torch.Tensor, q2: Optional[torch.Tensor],
-         k2: Optional[torch.Tensor], v: torch.Tensor, doc_ids: torch.Tensor, row_scale: torch.Tensor,
-         coef: Optional[torch.Tensor], b: Optional[torch.Tensor]) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
-    o, dstart, qend, *_ = _run_forward(kind, degree if degree > 0 else None, q1, k1, q2, k2, v, doc_ids, row_scale,
-                                       coef, b, out_like_v=False)
-    return o, dstart, qend
+         k2: Optional[torch.Tensor], v: torch.Tensor, doc_start: torch.Tensor, query_end: torch.Tensor,
+         row_scale: torch.Tensor, coef: Optional[torch.Tensor], b: Optional[torch.Tensor]) -> torch.Tensor:
+    o, *_ = _run_forward(kind, degree if degree > 0 else None, q1, k1, q2, k2, v, doc_start, row_scale, coef, b,
+                         out_like_v=False, bounds=(doc_start, query_end))
+    return o
 
 
 @_fwd.register_fake
-def _fwd_fake(kind, degree, q1, k1, q2, k2, v, doc_ids, row_scale, coef, b):
-    B, T = doc_ids.shape
-    o = v.new_empty(v.shape)
-    return o, doc_ids.new_empty((B, T), dtype=torch.int32), doc_ids.new_empty((B, T), dtype=torch.int32)
+def _fwd_fake(kind, degree, q1, k1, q2, k2, v, doc_start, query_end, row_scale, coef, b):
+    return v.new_empty(v.shape)
 
 
 @torch.library.custom_op("tnpa::poly_attention_backward", mutates_args=())
@@ -71,15 +81,14 @@ def _bwd_fake(kind, degree, q1, k1, q2, k2, v, doc_start, query_end, row_scale, 
 
 
 def _setup_context(ctx, inputs, output):
-    kind, degree, q1, k1, q2, k2, v, doc_ids, row_scale, coef, b = inputs
-    _, dstart, qend = output
+    kind, degree, q1, k1, q2, k2, v, dstart, qend, row_scale, coef, b = inputs
     ctx.kind, ctx.degree = kind, degree
     ctx.coef_dtype = coef.dtype if coef is not None else None
     ctx.b_dtype = b.dtype if b is not None else None
     ctx.save_for_backward(q1, k1, q2, k2, v, dstart, qend, row_scale, coef, b)
 
 
-def _backward(ctx, do, _dstart_grad, _qend_grad):
+def _backward(ctx, do):
     q1, k1, q2, k2, v, dstart, qend, row_scale, coef, b = ctx.saved_tensors
     kind = ctx.kind
     dq1, dk1, dq2, dk2, dv, dpar = _bwd(kind, ctx.degree, q1, k1, q2, k2, v, dstart, qend, row_scale, coef, b,
@@ -87,18 +96,18 @@ def _backward(ctx, do, _dstart_grad, _qend_grad):
     two = kind in _TWO_PAIRS
     dcoef = dpar.to(ctx.coef_dtype) if (kind == _abi.LOWER_DEGREE_MIX and coef is not None) else None
     db = dpar[:, 0].to(ctx.b_dtype) if (kind == _abi.OFFSET_SQUARE and b is not None) else None
-    return (None, None, dq1, dk1, dq2 if two else None, dk2 if two else None, dv, None, None, dcoef, db)
+    return (None, None, dq1, dk1, dq2 if two else None, dk2 if two else None, dv, None, None, None, dcoef, db)
 
 
 _fwd.register_autograd(_backward, setup_context=_setup_context)
 
 
-def poly_attention_op(kind, q1, k1, q2, k2, v, doc_ids, row_scale, coef=None, b=None, *, degree=None):
+def poly_attention_op(kind, q1, k1, q2, k2, v, doc_ids, row_scale, coef=None, b=None, *, degree=None, bounds=None):
     """poly_attention_hip through the registered custom ops (same arguments, same results; contiguous output).
     Unknown kinds raise KeyError, as the reference."""
     K, degree = _canonical(kind, q1, k1, q2, k2, degree)
     two = K in _TWO_PAIRS
-    o, _, _ = _fwd(K, int(degree) if degree is not None else 0, q1, k1, q2 if two else None, k2 if two else None,
-                   v, doc_ids, row_scale, coef if K == _abi.LOWER_DEGREE_MIX else None,
-                   b if K == _abi.OFFSET_SQUARE else None)
-    return o
+    dstart, qend = doc_bounds_op(doc_ids) if bounds is None else bounds
+    return _fwd(K, int(degree) if degree is not None else 0, q1, k1, q2 if two else None, k2 if two else None,
+                v, dstart, qend, row_scale, coef if K == _abi.LOWER_DEGREE_MIX else None,
+                b if K == _abi.OFFSET_SQUARE else None)

@@ -30,9 +30,10 @@ _TWO_PAIRS = (_abi.SIGNED_PRODUCT, _abi.LOWER_DEGREE_MIX)
 
 
 def _aligned_rows(x: torch.Tensor) -> bool:
-    """Unit stride on the head dim and 16-byte aligned rows, as the kernels' 128-bit loads require."""
+    """Unit stride on the head dim, rows that do not overlap (a time stride of at least the head dim: a dO reduced
+    or broadcast over time has stride 0) and 16-byte aligned rows, as the kernels' 128-bit loads require."""
     es = x.element_size()
-    if x.stride(-1) != 1 or x.data_ptr() % 16 or (x.stride(2) * es) % 16:
+    if x.stride(-1) != 1 or x.stride(2) < x.shape[-1] or x.data_ptr() % 16 or (x.stride(2) * es) % 16:
         return False
     if x.shape[0] > 1 and (x.stride(0) * es) % 16:
         return False
@@ -57,15 +58,21 @@ def _stream(dev: torch.device) -> ctypes.c_void_p:
 def doc_bounds(doc_ids: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
     """(doc_start, query_end) int32 (B, T): first key visible from each query (q + 1 for padding) and one past the
     last query that sees each key. Replaces ref: tnlm/kernels/poly_attn.py:205-218 (_block_bounds); int64 ids are
-    read as int64 (no narrowing)."""
+    read as int64 (no narrowing). A model computes them once per batch and hands them to every layer's call
+    (`bounds=`), instead of each layer recomputing them from the same ids."""
+    if torch.compiler.is_compiling():
+        from .ops import doc_bounds_op
+        return doc_bounds_op(doc_ids)
     doc = doc_ids
     if doc.dtype not in (torch.int32, torch.int64):
         doc = doc.long()
     if doc.dim() != 2:
         raise ValueError(f"doc_ids must be (B, T), got {tuple(doc.shape)}")
-    if doc.stride(1) != 1:
-        doc = doc.contiguous()
+    if not doc.is_cuda:
+        raise ValueError("poly_attention_hip needs tensors on a ROCm device (doc_ids is on the CPU)")
     B, T = doc.shape
+    if doc.stride(1) != 1 or (B > 1 and doc.stride(0) < T):  # e.g. ids expanded over the batch (stride 0)
+        doc = doc.contiguous()
     dstart = torch.empty(B, T, dtype=torch.int32, device=doc.device)
     qend = torch.empty(B, T, dtype=torch.int32, device=doc.device)
     lib = _abi.load()
@@ -119,16 +126,29 @@ def _canonical(kind, q1, k1, q2, k2, degree):
     return K, degree
 
 
-def _run_forward(K, degree, q1, k1, q2, k2, v, doc_ids, row_scale, coef, b, out_like_v=True):
-    """Validates, computes the document bounds and launches the forward. Returns (o, dstart, qend, (q1, k1, q2, k2,
-    v) as the kernels read them, sc, coef_f, b_f). o has v's strides (out_like_v) or is contiguous."""
+def _check_bounds(bounds, doc_ids):
+    """(doc_start, query_end) as doc_bounds(doc_ids) returns them: int32 (B, T), contiguous, on doc_ids' device."""
+    if not (isinstance(bounds, (tuple, list)) and len(bounds) == 2):
+        raise ValueError("bounds must be the (doc_start, query_end) pair from doc_bounds(doc_ids)")
+    for t in bounds:
+        if (t.dtype != torch.int32 or tuple(t.shape) != tuple(doc_ids.shape) or not t.is_contiguous()
+                or t.device != doc_ids.device):
+            raise ValueError("bounds must be the (doc_start, query_end) pair from doc_bounds(doc_ids): int32 (B, T) "
+                             "contiguous tensors on doc_ids' device")
+    return bounds[0], bounds[1]
+
+
+def _run_forward(K, degree, q1, k1, q2, k2, v, doc_ids, row_scale, coef, b, out_like_v=True, bounds=None):
+    """Validates, computes the document bounds (unless given) and launches the forward. Returns (o, dstart, qend,
+    (q1, k1, q2, k2, v) as the kernels read them, sc, coef_f, b_f). o has v's strides (out_like_v) or is
+    contiguous."""
     _validate(K, q1, k1, q2, k2, v, doc_ids, row_scale, coef, b, degree)
     q1, k1, v = _prep(q1), _prep(k1), _prep(v)
     if K in _TWO_PAIRS:
         q2, k2 = _prep(q2), _prep(k2)
     else:
         q2, k2 = q1, k1
-    dstart, qend = doc_bounds(doc_ids)
+    dstart, qend = doc_bounds(doc_ids) if bounds is None else _check_bounds(bounds, doc_ids)
     sc = row_scale.detach().float().contiguous()
     coef_f = coef.detach().float().contiguous() if K == _abi.LOWER_DEGREE_MIX else None
     b_f = b.detach().float().contiguous() if K == _abi.OFFSET_SQUARE else None
@@ -155,18 +175,14 @@ def _run_backward(K, degree, q1, k1, q2, k2, v, dstart, qend, sc, coef_f, b_f, d
     prob = _problem(K, degree, q1, k1, q2, k2, v, dstart, qend, sc, coef_f, b_f)
     lib = _abi.load()
     par = K in (_abi.OFFSET_SQUARE, _abi.LOWER_DEGREE_MIX)
-    ws = dpar = None
-    if par:
-        ws = torch.empty(max(1, lib.tnpa_dpar_workspace_floats(ctypes.byref(prob))), dtype=torch.float32,
-                         device=q1.device)
-        dpar = torch.empty(H, 4, dtype=torch.float32, device=q1.device)
-    # row_scale * dO, written by the library before its dK/dV pass and streamed by it, where that beats the pass
-    # scaling dO itself
-    dos = (torch.empty(do.shape, dtype=do.dtype, device=do.device)
-           if lib.tnpa_dout_scaled_helps(ctypes.byref(prob)) else None)
+    dpar = torch.empty(H, 4, dtype=torch.float32, device=q1.device) if par else None
+    # the library's scratch (dcoef/db partials; the row-scaled dO where the plan streams it), caller-allocated
+    nbytes = lib.tnpa_backward_workspace_bytes(ctypes.byref(prob))
+    if nbytes < 0:
+        _abi.check(_abi.ERR_INVALID, "poly_attention backward")
+    ws = torch.empty(nbytes, dtype=torch.uint8, device=q1.device) if nbytes > 0 else None
     g = _abi.Grads(_desc(do), _desc(dq1), _desc(dk1), _desc(dq2), _desc(dk2), _desc(dv),
-                   ws.data_ptr() if par else None, dpar.data_ptr() if par else None,
-                   _desc(dos) if dos is not None else _abi.Tensor())
+                   dpar.data_ptr() if par else None, ws.data_ptr() if ws is not None else None, nbytes)
     with torch.cuda.device(q1.device):
         _abi.check(lib.tnpa_backward(ctypes.byref(prob), ctypes.byref(g), _stream(q1.device)),
                    "poly_attention backward")
@@ -179,11 +195,11 @@ class PolyAttention(torch.autograd.Function):
     """ref: tnlm/kernels/poly_attn.py:255-309, with an appended `degree` argument for kind="power"."""
 
     @staticmethod
-    def forward(ctx, kind, q1, k1, q2, k2, v, doc_ids, row_scale, coef, b, degree=None):
+    def forward(ctx, kind, q1, k1, q2, k2, v, doc_ids, row_scale, coef, b, degree=None, bounds=None):
         shared = KINDS[kind] == _abi.SIGNED_PRODUCT and q2 is q1 and k2 is k1
         K, degree = _canonical(kind, q1, k1, q2, k2, degree)
         o, dstart, qend, (q1, k1, q2, k2, v), sc, coef_f, b_f = _run_forward(
-            K, degree, q1, k1, q2, k2, v, doc_ids, row_scale, coef, b)
+            K, degree, q1, k1, q2, k2, v, doc_ids, row_scale, coef, b, bounds=bounds)
         ctx.save_for_backward(q1, k1, q2, k2, v, dstart, qend, sc, coef_f, b_f)
         ctx.K, ctx.degree, ctx.shared = K, degree, shared
         ctx.has_coef, ctx.has_b = coef is not None, b is not None
@@ -199,7 +215,7 @@ class PolyAttention(torch.autograd.Function):
                                                       b_f, do)
         dcoef = dpar.to(ctx.coef_dtype) if (K == _abi.LOWER_DEGREE_MIX and ctx.has_coef) else None
         db = dpar[:, 0].to(ctx.b_dtype) if (K == _abi.OFFSET_SQUARE and ctx.has_b) else None
-        return None, dq1, dk1, dq2, dk2, dv, None, None, dcoef, db, None
+        return None, dq1, dk1, dq2, dk2, dv, None, None, dcoef, db, None, None
 
 
 def _alloc_like(x: torch.Tensor) -> torch.Tensor:
@@ -216,12 +232,14 @@ def _problem(K, degree, q1, k1, q2, k2, v, dstart, qend, sc, coef_f, b_f) -> _ab
                         b_f.data_ptr() if b_f is not None else None)
 
 
-def poly_attention_hip(kind, q1, k1, q2, k2, v, doc_ids, row_scale, coef=None, b=None, *, degree=None):
+def poly_attention_hip(kind, q1, k1, q2, k2, v, doc_ids, row_scale, coef=None, b=None, *, degree=None,
+                       bounds=None):
     """q*, k*: (B, H, T, dk); v: (B, H, T, dv); doc_ids: (B, T) contiguous ids, < 0 = padding;
     row_scale: (B, T) = n_visible^-p for real queries, 0 for padding. kind="power" takes degree=p and ignores
-    q2/k2. Every gradient is reduced in a fixed order (deterministic).  ref: tnlm/kernels/poly_attn.py:312-315"""
+    q2/k2. bounds: optional doc_bounds(doc_ids), computed once per batch by a caller with many layers. Every
+    gradient is reduced in a fixed order (deterministic).  ref: tnlm/kernels/poly_attn.py:312-315"""
     if torch.compiler.is_compiling():
         # under torch.compile the same kernels run behind registered custom ops (opaque to the compiler)
         from .ops import poly_attention_op
-        return poly_attention_op(kind, q1, k1, q2, k2, v, doc_ids, row_scale, coef, b, degree=degree)
-    return PolyAttention.apply(kind, q1, k1, q2, k2, v, doc_ids, row_scale, coef, b, degree)
+        return poly_attention_op(kind, q1, k1, q2, k2, v, doc_ids, row_scale, coef, b, degree=degree, bounds=bounds)
+    return PolyAttention.apply(kind, q1, k1, q2, k2, v, doc_ids, row_scale, coef, b, degree, bounds)

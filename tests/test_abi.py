@@ -16,6 +16,7 @@ import torch
 
 ROOT = Path(__file__).resolve().parents[1]
 HEADER = ROOT / "include" / "tnpa.h"
+INTERNAL = ROOT / "tensor_train_ing_amd" / "csrc" / "tnpa_internal.h"
 
 
 @pytest.fixture(scope="module")
@@ -24,24 +25,30 @@ def lib():
     return _abi.load()
 
 
-def _declared_functions():
-    text = HEADER.read_text()
+def _declared_functions(header=HEADER):
+    text = header.read_text()
     text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
     return sorted(set(re.findall(r"^\s*[\w\s\*]+?\b(tnpa_\w+)\s*\(", text, flags=re.M)))
 
 
 def test_library_loads_and_reports_abi_version(lib):
     from tensor_train_ing_amd import _abi
-    assert lib.tnpa_abi_version() == _abi.ABI_VERSION == 2
+    assert lib.tnpa_abi_version() == _abi.ABI_VERSION == 3
 
 
 def test_every_declared_symbol_is_exported(lib):
     names = _declared_functions()
-    assert len(names) >= 7, names
+    assert len(names) >= 6, names
     for n in names:
         assert hasattr(lib, n), n
     from tensor_train_ing_amd import _abi
     assert set(_abi._SIGNATURES) == set(names)
+    # the launch-level entry points the benchmark and the tests use stay out of the public header
+    internal = _declared_functions(INTERNAL)
+    assert internal and not set(internal) & set(names)
+    for n in internal:
+        assert hasattr(lib, n), n
+    assert set(_abi._INTERNAL) == set(internal)
 
 
 @pytest.mark.skipif(shutil.which("gcc") is None, reason="needs gcc")
@@ -56,8 +63,8 @@ int main(void) {
   printf("%zu %zu %zu\n", sizeof(tnpa_tensor_t), sizeof(tnpa_problem_t), sizeof(tnpa_grads_t));
   printf("%zu %zu %zu %zu\n", offsetof(tnpa_problem_t, q1), offsetof(tnpa_problem_t, v),
          offsetof(tnpa_problem_t, doc_start), offsetof(tnpa_problem_t, offset));
-  printf("%zu %zu %zu\n", offsetof(tnpa_grads_t, dv), offsetof(tnpa_grads_t, dpar),
-         offsetof(tnpa_grads_t, dout_scaled));
+  printf("%zu %zu %zu %zu\n", offsetof(tnpa_grads_t, dv), offsetof(tnpa_grads_t, dpar),
+         offsetof(tnpa_grads_t, workspace), offsetof(tnpa_grads_t, workspace_bytes));
   return 0;
 }''')
     exe = tmp_path / "layout"
@@ -68,7 +75,7 @@ int main(void) {
     P, G = _abi.Problem, _abi.Grads
     assert got[0] == [ctypes.sizeof(_abi.Tensor), ctypes.sizeof(P), ctypes.sizeof(G)]
     assert got[1] == [P.q1.offset, P.v.offset, P.doc_start.offset, P.offset.offset]
-    assert got[2] == [G.dv.offset, G.dpar.offset, G.dout_scaled.offset]
+    assert got[2] == [G.dv.offset, G.dpar.offset, G.workspace.offset, G.workspace_bytes.offset]
 
 
 def _problem(**kw):
@@ -114,55 +121,76 @@ def test_misaligned_views_and_missing_parameters_are_rejected(lib):
     assert lib.tnpa_forward(ctypes.byref(p), ctypes.byref(out), None) == _abi.ERR_INVALID
     assert "offset" in lib.tnpa_last_error().decode()
     assert lib.tnpa_forward(None, ctypes.byref(out), None) == _abi.ERR_INVALID
-    # backward: the two head-scalar kinds need the dpar buffers
+    # backward: the two head-scalar kinds need dpar and a workspace of the size the library asks for
     p = _problem(kind=_abi.OFFSET_SQUARE, offset=4096)
     t = _abi.Tensor(4096, 2 * 128 * 64, 128 * 64, 64)
-    g = _abi.Grads(t, t, t, t, t, t, None, None)
+    need = lib.tnpa_backward_workspace_bytes(ctypes.byref(p))
+    assert need > 0
+    g = _abi.Grads(t, t, t, t, t, t, None, 4096, need)
     assert lib.tnpa_backward(ctypes.byref(p), ctypes.byref(g), None) == _abi.ERR_INVALID
     assert "dpar" in lib.tnpa_last_error().decode()
-    assert lib.tnpa_backward_phase(ctypes.byref(_problem()), ctypes.byref(g), 0, None) == _abi.ERR_INVALID
-    assert lib.tnpa_backward_phase(ctypes.byref(_problem()), ctypes.byref(g), 32, None) == _abi.ERR_INVALID
-    # the key-side parts: not together with the whole key side, the scaling part needs its workspace, and only the
-    # split configurations (16-bit, one q/k pair) run dV or dK alone
-    both = _abi.PHASE_KV | _abi.PHASE_KV_DV
-    assert lib.tnpa_backward_phase(ctypes.byref(_problem()), ctypes.byref(g), both, None) == _abi.ERR_INVALID
-    assert lib.tnpa_backward_phase(ctypes.byref(_problem()), ctypes.byref(g), _abi.PHASE_KV_SCALE,
-                                   None) == _abi.ERR_INVALID
-    assert "dout_scaled" in lib.tnpa_last_error().decode()
-    f32 = _problem(dtype=_abi.F32)
-    assert lib.tnpa_backward_phase(ctypes.byref(f32), ctypes.byref(g), _abi.PHASE_KV_DV, None) == _abi.ERR_UNSUPPORTED
-    two = _problem(kind=_abi.SIGNED_PRODUCT)
-    assert lib.tnpa_backward_phase(ctypes.byref(two), ctypes.byref(g), _abi.PHASE_KV_DK, None) == _abi.ERR_UNSUPPORTED
+    g = _abi.Grads(t, t, t, t, t, t, 4096, 4096, need - 1)
+    assert lib.tnpa_backward(ctypes.byref(p), ctypes.byref(g), None) == _abi.ERR_INVALID
+    assert "workspace" in lib.tnpa_last_error().decode()
+    g = _abi.Grads(t, t, t, t, t, t, 4096, 4096 + 16, need)
+    assert lib.tnpa_backward(ctypes.byref(p), ctypes.byref(g), None) == _abi.ERR_INVALID
+    assert "aligned" in lib.tnpa_last_error().decode()
+    g = _abi.Grads(t, t, t, t, t, t, None, None, 0)
+    assert lib.tnpa_backward_workspace_bytes(None) == -1
+    assert lib.tnpa_backward(None, ctypes.byref(g), None) == _abi.ERR_INVALID
+    # internal launch-level entry: options and launch index are checked
+    assert lib.tnpa_x_backward(ctypes.byref(_problem()), ctypes.byref(g), 3, -1, None) == _abi.ERR_INVALID
+    assert lib.tnpa_x_backward(ctypes.byref(_problem()), ctypes.byref(g), 0, 7, None) == _abi.ERR_INVALID
+    assert lib.tnpa_x_launches(ctypes.byref(_problem()), 8) == -1
     assert lib.tnpa_doc_bounds(None, 1, 128, 2, 128, None, None, None) == _abi.ERR_INVALID
     assert lib.tnpa_doc_bounds(ctypes.c_void_p(4096), 1, 64, 2, 128, ctypes.c_void_p(4096), ctypes.c_void_p(4096),
                                None) == _abi.ERR_INVALID
 
 
-def test_dpar_workspace_size(lib):
+def test_backward_workspace_size(lib):
+    """The workspace holds the fixed-order dcoef/db partials (one float4 per (b, h, key block)) and, where the plan
+    streams it, row_scale * dO in the problem dtype; each part rounded up to 256 bytes."""
     from tensor_train_ing_amd import _abi
-    assert lib.tnpa_dpar_workspace_floats(ctypes.byref(_problem())) == 0
-    p = _problem(kind=_abi.LOWER_DEGREE_MIX, seq_len=300)
-    assert lib.tnpa_dpar_workspace_floats(ctypes.byref(p)) == 2 * 2 * 3 * 4  # ceil(300 / 128) key blocks
-    p = _problem(kind=_abi.OFFSET_SQUARE, seq_len=300)  # bf16, one pair, head dim 64: four-wave 128-key blocks
-    assert lib.tnpa_dpar_workspace_floats(ctypes.byref(p)) == 2 * 2 * 3 * 4
-    p = _problem(kind=_abi.OFFSET_SQUARE, seq_len=300, head_dim_k=128, head_dim_v=128)  # eight-wave 256-key blocks
-    assert lib.tnpa_dpar_workspace_floats(ctypes.byref(p)) == 2 * 2 * 2 * 4
+    r = lambda n: -(-n // 256) * 256  # noqa: E731
+    assert lib.tnpa_backward_workspace_bytes(ctypes.byref(_problem())) == 0
+    p = _problem(kind=_abi.OFFSET_SQUARE, offset=4096, seq_len=300)  # bf16, head dim 64: four-wave 128-key blocks
+    assert lib.tnpa_backward_workspace_bytes(ctypes.byref(p)) == r(2 * 2 * 3 * 4 * 4)
+    p = _problem(kind=_abi.OFFSET_SQUARE, offset=4096, seq_len=300, head_dim_k=128, head_dim_v=128)  # 256-key blocks
+    assert lib.tnpa_backward_workspace_bytes(ctypes.byref(p)) == r(2 * 2 * 2 * 4 * 4)
+    # lower_degree_mix (two pairs) streams the row-scaled dO: partials, then (B, H, T, dv) bf16
+    p = _problem(kind=_abi.LOWER_DEGREE_MIX, coef=4096, seq_len=300)
+    assert lib.tnpa_backward_workspace_bytes(ctypes.byref(p)) == r(2 * 2 * 3 * 4 * 4) + r(2 * 2 * 300 * 64 * 2)
+    # forcing the row-scaled dO on or off changes only that part
+    p = _problem()
+    assert lib.tnpa_x_workspace_bytes(ctypes.byref(p), _abi.X_PRESCALE_ON) == r(2 * 2 * 128 * 64 * 2)
+    p = _problem(dtype=_abi.F32)
+    assert lib.tnpa_x_workspace_bytes(ctypes.byref(p), _abi.X_PRESCALE_OFF) == 0
+    assert lib.tnpa_x_workspace_bytes(ctypes.byref(p), 0) == r(2 * 2 * 128 * 64 * 4)
 
 
-def test_dout_scaled_helps_only_where_the_passes_cannot_scale_for_free(lib):
+def _launches(lib, p, opts=0):
+    return [lib.tnpa_x_launch_name(ctypes.byref(p), opts, i).decode() for i in range(lib.tnpa_x_launches(
+        ctypes.byref(p), opts))]
+
+
+def test_backward_plan(lib):
+    """Which launches tnpa_backward makes: the row-scaled dO only where the key side cannot scale dO for free (fp32,
+    two q/k pairs, or a head dim too small for the three-buffer tile split); separate dV and dK passes for 16-bit one
+    q/k pair at a head dim above 64; the dpar reduction for the kinds with head parameters."""
     from tensor_train_ing_amd import _abi
-    assert lib.tnpa_dout_scaled_helps(None) == 0
-    # 16-bit, one q/k pair, tiles that split evenly over the threads (head dims 32 or 64 with four-wave workgroups,
-    # 64 or 128 with eight-wave ones): the dK/dV passes scale dO as they write it to LDS
-    assert lib.tnpa_dout_scaled_helps(ctypes.byref(_problem())) == 0
-    assert lib.tnpa_dout_scaled_helps(ctypes.byref(_problem(dtype=_abi.F16, kind=_abi.OFFSET_SQUARE))) == 0
-    assert lib.tnpa_dout_scaled_helps(ctypes.byref(_problem(head_dim_v=32))) == 0
-    assert lib.tnpa_dout_scaled_helps(ctypes.byref(_problem(head_dim_k=128, head_dim_v=128))) == 0
-    # fp32, two q/k pairs, or a head dim too small for the tile split: the pre-scaled workspace is faster
-    assert lib.tnpa_dout_scaled_helps(ctypes.byref(_problem(dtype=_abi.F32))) == 1
-    assert lib.tnpa_dout_scaled_helps(ctypes.byref(_problem(kind=_abi.SIGNED_PRODUCT))) == 1
-    assert lib.tnpa_dout_scaled_helps(ctypes.byref(_problem(head_dim_v=16))) == 1
-    assert lib.tnpa_dout_scaled_helps(ctypes.byref(_problem(head_dim_k=128, head_dim_v=32))) == 1
+    assert _launches(lib, _problem()) == ["kv", "q"]
+    assert _launches(lib, _problem(head_dim_k=128, head_dim_v=128)) == ["dv", "dk", "q"]
+    assert _launches(lib, _problem(dtype=_abi.F16, head_dim_k=128, head_dim_v=128)) == ["dv", "dk", "q"]
+    assert _launches(lib, _problem(dtype=_abi.F32)) == ["scale", "kv", "q"]
+    assert _launches(lib, _problem(kind=_abi.SIGNED_PRODUCT)) == ["scale", "kv", "q"]
+    assert _launches(lib, _problem(head_dim_v=16)) == ["scale", "kv", "q"]
+    assert _launches(lib, _problem(head_dim_k=128, head_dim_v=32)) == ["scale", "dv", "dk", "q"]
+    assert _launches(lib, _problem(head_dim_v=32)) == ["kv", "q"]
+    assert _launches(lib, _problem(kind=_abi.OFFSET_SQUARE, offset=4096)) == ["kv", "q", "dpar"]
+    assert _launches(lib, _problem(kind=_abi.LOWER_DEGREE_MIX, coef=4096)) == ["scale", "kv", "q", "dpar"]
+    assert _launches(lib, _problem(), _abi.X_PRESCALE_ON) == ["scale", "kv", "q"]
+    assert _launches(lib, _problem(dtype=_abi.F32), _abi.X_PRESCALE_OFF) == ["kv", "q"]
+    assert lib.tnpa_x_launch_name(ctypes.byref(_problem()), 0, 5) == b""
 
 
 def test_python_operator_errors_mirror_the_reference():

@@ -15,9 +15,11 @@ def test_custom_ops_are_registered_with_the_reference_argument_order():
     import tensor_train_ing_amd  # noqa: F401  (registers tnpa::*)
     fwd = str(torch.ops.tnpa.poly_attention.default._schema)
     bwd = str(torch.ops.tnpa.poly_attention_backward.default._schema)
-    assert "Tensor q1, Tensor k1, Tensor? q2, Tensor? k2, Tensor v, Tensor doc_ids, Tensor row_scale, " \
-           "Tensor? coef, Tensor? b" in fwd
-    assert fwd.endswith("-> (Tensor, Tensor, Tensor)")
+    bounds = str(torch.ops.tnpa.doc_bounds.default._schema)
+    assert "Tensor q1, Tensor k1, Tensor? q2, Tensor? k2, Tensor v, Tensor doc_start, Tensor query_end, " \
+           "Tensor row_scale, Tensor? coef, Tensor? b" in fwd
+    assert fwd.endswith("-> Tensor")
+    assert "Tensor doc_ids" in bounds and bounds.endswith("-> (Tensor, Tensor)")
     assert "Tensor dout" in bwd and bwd.endswith("-> (Tensor, Tensor, Tensor, Tensor, Tensor, Tensor)")
 
 
@@ -31,10 +33,11 @@ def test_fake_shapes(kind, two, par):
         v = torch.empty(2, 3, 40, 16, dtype=torch.bfloat16)
         doc = torch.zeros(2, 40, dtype=torch.long)
         rs = torch.ones(2, 40)
-        o, ds, qe = torch.ops.tnpa.poly_attention(kind, 2, q, q, q if two else None, q if two else None, v, doc, rs,
-                                                  None, None)
-        assert o.shape == v.shape and o.dtype == v.dtype and o.is_contiguous()
+        ds, qe = torch.ops.tnpa.doc_bounds(doc)
         assert ds.shape == qe.shape == (2, 40) and ds.dtype == torch.int32
+        o = torch.ops.tnpa.poly_attention(kind, 2, q, q, q if two else None, q if two else None, v, ds, qe, rs,
+                                          None, None)
+        assert o.shape == v.shape and o.dtype == v.dtype and o.is_contiguous()
         g = torch.ops.tnpa.poly_attention_backward(kind, 2, q, q, q if two else None, q if two else None, v, ds, qe,
                                                    rs, None, None, v)
         assert [tuple(x.shape) for x in g[:2]] == [tuple(q.shape)] * 2
@@ -99,7 +102,10 @@ def test_bench_refuses_more_than_one_gpu(capsys):
 
 
 def test_bench_cpu_baseline_runs_on_a_small_sample():
-    """The CPU-baseline leg (the oracle timed on host cores) on a tiny workload: a positive rate and its sample."""
+    """The CPU-baseline leg (the float32 torch restatement timed on host cores) on a tiny workload drawn as the GPU
+    run draws it: positive fwd and fwd+bwd rates, the CPU model and the sample."""
     import bench
-    r = bench.cpu_baseline(1, 2, 64, 16, 2, 0.5)
-    assert r["value"] > 0 and r["kind"] == "port" and r["cores"] >= 1 and "slices" in r["sample"]
+    q, k, v, do, doc, rs = bench.make_inputs(1, 2, 64, 16, 0.0, 0, "cpu")
+    r = bench.cpu_baseline(q, k, v, do, rs, 2, 0.5)
+    assert r["value"] > 0 and r["fwd_tflops"] > 0 and r["kind"] == "port" and r["cores"] >= 1
+    assert "slices" in r["sample"] and r["cpu"]

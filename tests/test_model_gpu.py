@@ -55,25 +55,52 @@ def test_model_hip_backend_matches_reference(kind, mlp, degree):
         assert _rel(b.grad, a.grad) < 1e-3, (n, _rel(b.grad, a.grad))
 
 
-@pytest.mark.parametrize("kind", ["signed_product", "offset_square", "lower_degree_mix", "power"])
-def test_compiled_model_matches_eager(kind):
+@pytest.mark.parametrize("kind,backend", [("signed_product", "aot_eager"), ("offset_square", "aot_eager"),
+                                          ("lower_degree_mix", "aot_eager"), ("power", "aot_eager"),
+                                          ("power", "inductor")])
+def test_compiled_model_matches_eager(kind, backend):
     """torch.compile(fullgraph=True) traces the model with the operator as opaque tnpa:: custom ops (a graph break
-    would raise); loss and gradients equal the eager run's."""
+    would raise); loss and gradients equal the eager run's. "inductor" is torch.compile's default backend, the one
+    the reference trains with (ref: tnlm/train.py:353); it regenerates the model's other ops, so its tolerance is
+    that of the model parity test rather than the bitwise-level 1e-5 of aot_eager."""
     dev = torch.device("cuda:0")
-    print(f"[compiled model] kind={kind}", flush=True)
+    print(f"[compiled model] kind={kind} backend={backend}", flush=True)
     torch._dynamo.reset()
     _, eager = _pair(kind, "bilinear", dev)
     _, comp = _pair(kind, "bilinear", dev)
     idx, doc, tgt = _batch(dev)
     _, le = eager(idx, doc, tgt)
     le.backward()
-    fn = torch.compile(comp, backend="aot_eager", fullgraph=True)
+    fn = torch.compile(comp, backend=backend, fullgraph=True)
     _, lc = fn(idx, doc, tgt)
     lc.backward()
     torch.cuda.synchronize()
-    assert abs(le.item() - lc.item()) <= 1e-6 * abs(le.item())
+    ltol, gtol = (1e-6, 1e-5) if backend == "aot_eager" else (1e-4, 1e-3)
+    assert abs(le.item() - lc.item()) <= ltol * abs(le.item())
     for (n, a), (_, b) in zip(eager.named_parameters(), comp.named_parameters()):
-        assert _rel(b.grad, a.grad) < 1e-5, (n, _rel(b.grad, a.grad))
+        assert _rel(b.grad, a.grad) < gtol, (n, _rel(b.grad, a.grad))
+
+
+def test_document_bounds_computed_once_per_forward(monkeypatch):
+    """A four-layer model runs the document-bounds prepass once per forward (the model context computes it and
+    every layer's call receives it), and the backward reuses the forward's bounds."""
+    import tensor_train_ing_amd.poly_attn as pa
+    dev = torch.device("cuda:0")
+    calls = []
+    orig = pa.doc_bounds
+
+    def counting(doc_ids):
+        calls.append(tuple(doc_ids.shape))
+        return orig(doc_ids)
+
+    monkeypatch.setattr(pa, "doc_bounds", counting)
+    torch.manual_seed(0)
+    model = MiniLM("power", "bilinear", layers=4, backend="hip").to(dev)
+    idx, doc, tgt = _batch(dev)
+    _, loss = model(idx, doc, tgt)
+    loss.backward()
+    torch.cuda.synchronize()
+    assert calls == [(2, 100)]
 
 
 @pytest.mark.parametrize("kind", ["signed_product", "offset_square", "lower_degree_mix", "power"])

@@ -224,6 +224,28 @@ def test_doc_bounds_bruteforce_and_reference_block_bounds():
                 assert (start[bb][::BM] >= lo[bb]).all()
 
 
+# hand-derived bounds (ids, doc_start, query_end, {(BM, BN): (LO, HI)}): exact values, so a bound that is too loose
+# or too tight fails, not only one that misses a visible pair
+HAND = [
+    ([0, 0, 0, 1, 1, -1, -1, 2], [0, 0, 0, 3, 3, 6, 7, 7], [3, 3, 3, 5, 5, 5, 6, 8],
+     {(4, 4): ([0, 3], [5, 8]), (2, 2): ([0, 0, 3, 5], [3, 5, 7, 8]), (3, 3): ([0, 3, 5], [3, 7, 8])}),
+    ([0, 0, 0, 0, 0], [0, 0, 0, 0, 0], [5, 5, 5, 5, 5], {(2, 2): ([0, 0, 0], [5, 5, 5])}),
+    ([-1, -1, -1], [1, 2, 3], [0, 1, 2], {(2, 2): ([0, 0], [3, 3])}),
+    ([0, 1, 2, 3], [0, 1, 2, 3], [1, 2, 3, 4], {(2, 2): ([0, 2], [2, 4])}),
+    ([5, 5, -1, 7, 7, 7], [0, 0, 3, 3, 3, 3], [2, 2, 2, 6, 6, 6], {(2, 4): ([0, 2, 3], [6, 6])}),
+]
+
+
+@pytest.mark.parametrize("case", range(len(HAND)))
+def test_doc_bounds_and_block_bounds_hand_derived(case):
+    ids, start, qend, blocks = HAND[case]
+    ds, qe = doc_bounds(np.array([ids]))
+    assert ds.tolist() == [start] and qe.tolist() == [qend]
+    for (BM, BN), (lo, hi) in blocks.items():
+        rl, rh = block_bounds_reference(np.array([ids]), BM, BN)
+        assert rl.tolist() == [lo] and rh.tolist() == [hi], (BM, BN)
+
+
 def test_round_to_bf16_matches_torch():
     x = np.random.default_rng(8).standard_normal(10000).astype(np.float32) * 100
     ref = torch.from_numpy(x).to(torch.bfloat16).float().numpy()
@@ -266,3 +288,28 @@ def test_torch_reference_matches_oracle(kind):
     for n, e in exp.items():
         # the row scale the operator takes is fp32, so agreement is to fp32 rounding of the largest entries
         np.testing.assert_allclose(got[n].numpy(), e, rtol=1e-6, atol=1e-6 * np.abs(e).max(), err_msg=n)
+
+
+@pytest.mark.parametrize("kind,degree", [("power", 2), ("power", 4), ("signed_product", None),
+                                         ("offset_square", None), ("lower_degree_mix", None)])
+def test_torch_dense_baseline_matches_oracle(kind, degree):
+    """The torch restatement bench.py times as the CPU baseline equals the numpy oracle, forward and (through
+    autograd) backward, in float64 on one document with the (t+1)^-1/2 row scale."""
+    from oracle import causal_row_scale, dense_attention
+    rng = np.random.default_rng(31)
+    T, D = 40, 16
+    q1, k1, q2, k2, v, do = (rng.standard_normal((1, 1, T, D)) for _ in range(6))
+    coef, b = np.array([[0.3, -0.5, 0.7, 1.1]]), np.array([0.25])
+    rs = (np.arange(T) + 1.0) ** -0.5
+    C = np.tril(np.ones((T, T)))[None, None] * rs[None, None, :, None]
+    ref = polynomial_attention(kind, q1, k1, q2, k2, v, C, coef=coef, b=b, degree=degree)
+    g = polynomial_attention_backward(kind, q1, k1, q2, k2, v, C, do, coef=coef, b=b, degree=degree)
+    t = lambda x: torch.from_numpy(x[0, 0]).requires_grad_()  # noqa: E731
+    ins = [t(x) for x in (q1, k1, q2, k2, v)]
+    y = dense_attention(kind, *ins, causal_row_scale(torch.from_numpy(rs)), coef=torch.from_numpy(coef[0]),
+                        b=float(b[0]), degree=degree)
+    np.testing.assert_allclose(y.detach().numpy(), ref[0, 0], rtol=1e-10, atol=1e-10)
+    y.backward(torch.from_numpy(do[0, 0]))
+    for name, x in zip(("dq1", "dk1", "dq2", "dk2", "dv"), ins):
+        if name in g and g[name] is not None:
+            np.testing.assert_allclose(x.grad.numpy(), g[name][0, 0], rtol=1e-9, atol=1e-9)

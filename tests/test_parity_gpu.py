@@ -7,6 +7,7 @@ bound max|x - ref| / max|ref| <= 2e-2 per tensor (out, dq, dk, dv), with ref in 
 """
 from __future__ import annotations
 
+import ctypes
 import json
 from pathlib import Path
 
@@ -194,6 +195,98 @@ def test_float16_inputs():
     _check(compare(res, ref), BF16_FRO, BF16_MAX)
 
 
+def _finite(res):
+    for n, x in res.items():
+        assert torch.isfinite(x).all(), n
+
+
+@pytest.mark.parametrize("degree,qk_scale,boost", [(4, 128 ** -0.25, 0.01), (2, 1.0, 0.0), (4, 1.0, 0.0)])
+def test_float16_range_of_the_homogeneous_kinds(degree, qk_scale, boost):
+    """fp16 holds at most 65504: the score is scaled by 1/sqrt(dk) before the polynomial (as the reference's
+    S = q.k * sm), so P = S^p stays in range where the raw (q.k)^p would not. The p4-stress distribution (1% of rows
+    x4) reaches |q.k|^4 ~ 4e6 raw but S^4 ~ 260; unit-variance q/k at dk = 128 reach (q.k)^4 ~ 4e6 as well."""
+    print(f"[fp16 range] degree={degree} qk_scale={qk_scale:.3f} boost={boost}", flush=True)
+    q, k, _, _, v, dout = (x.cuda() if x is not None else None for x in gaussian_inputs(
+        1, 4, 512, 128, 128, torch.float16, 21, qk_scale=qk_scale, boost_rows=boost))
+    doc = torch.zeros(1, 512, dtype=torch.long, device="cuda")
+    rs = row_scale(doc, 0.5)
+    res = run_hip("power", q, k, None, None, v, dout, doc, rs, degree=degree)
+    _finite(res)
+    ref = dense_reference("power", q, k, None, None, v, dout, doc, rs, degree=degree)
+    _check(compare(res, ref, ["out", "dq1", "dk1", "dv"]), BF16_FRO, BF16_MAX)
+
+
+def test_float16_large_inputs_signed_product():
+    """The reference's large-input case (q1, k1 x30; ref: tests/test_kernels.py:84-93) in fp16: raw q1.k1 * q2.k2
+    would overflow fp16, S1 * S2 does not; outputs finite, padding rows zero, and within the fp16 tolerance of the
+    float64 reference."""
+    q1, k1, q2, k2, v, dout = (x.cuda() for x in gaussian_inputs(1, 1, 70, 64, 64, torch.float32, 22,
+                                                                 two_pairs=True))
+    q1, k1 = q1 * 30, k1 * 30
+    q1, k1, q2, k2, v, dout = (x.half() for x in (q1, k1, q2, k2, v, dout))
+    doc = torch.zeros(1, 70, dtype=torch.long, device="cuda")
+    doc[:, 60:] = -1
+    rs = row_scale(doc, 0.5)
+    res = run_hip("signed_product", q1, k1, q2, k2, v, dout, doc, rs)
+    _finite(res)
+    assert res["out"][:, :, 60:].abs().max() == 0
+    ref = dense_reference("signed_product", q1, k1, q2, k2, v, dout, doc, rs)
+    _check(compare(res, ref, ["out", "dq1", "dk1", "dq2", "dk2", "dv"]), BF16_FRO, BF16_MAX)
+
+
+def test_dout_with_zero_time_stride():
+    """A dO reduced over time (out.sum(dim=2)) has time stride 0: it is copied to rows the kernels can read, and the
+    gradients equal those of the same dO materialised."""
+    from tensor_train_ing_amd import poly_attention_hip
+    q, k, _, _, v, _ = (x.cuda() if x is not None else None for x in gaussian_inputs(
+        2, 2, 96, 64, 64, torch.bfloat16, 23, qk_scale=64 ** -0.25))
+    doc = torch.zeros(2, 96, dtype=torch.long, device="cuda")
+    rs = row_scale(doc, 0.5)
+    grads = []
+    for reduce in (True, False):
+        ins = [x.detach().clone().requires_grad_() for x in (q, k, v)]
+        out = poly_attention_hip("power", ins[0], ins[1], None, None, ins[2], doc, rs, degree=2)
+        if reduce:
+            y = out.sum(dim=2)  # its backward hands the operator ones expanded over time (stride 0)
+            y.backward(torch.ones_like(y))
+        else:
+            out.backward(torch.ones_like(out))
+        grads.append([x.grad for x in ins])
+    for a, b in zip(*grads):
+        assert torch.equal(a, b)
+
+
+def test_expanded_doc_ids():
+    """doc_ids expanded over the batch (batch stride 0) are read like their contiguous copy."""
+    from tensor_train_ing_amd.poly_attn import doc_bounds
+    row = torch.zeros(200, dtype=torch.long, device="cuda")
+    row[70:] = 1
+    row[180:] = -1
+    exp = row.expand(3, 200)
+    assert exp.stride(0) == 0
+    for a, b in zip(doc_bounds(exp), doc_bounds(exp.contiguous())):
+        assert torch.equal(a, b)
+
+
+# hand-derived per-token bounds: (ids, doc_start, query_end); padding rows see nothing (doc_start = t + 1) and
+# padding keys are seen by nobody (query_end = t)
+HAND_BOUNDS = [
+    ([0, 0, 0, 1, 1, -1, -1, 2], [0, 0, 0, 3, 3, 6, 7, 7], [3, 3, 3, 5, 5, 5, 6, 8]),
+    ([0, 0, 0, 0, 0], [0, 0, 0, 0, 0], [5, 5, 5, 5, 5]),
+    ([-1, -1, -1], [1, 2, 3], [0, 1, 2]),
+    ([0, 1, 2, 3], [0, 1, 2, 3], [1, 2, 3, 4]),
+    ([5, 5, -1, 7, 7, 7], [0, 0, 3, 3, 3, 3], [2, 2, 2, 6, 6, 6]),
+]
+
+
+@pytest.mark.parametrize("case", range(len(HAND_BOUNDS)))
+def test_doc_bounds_hand_derived(case):
+    from tensor_train_ing_amd.poly_attn import doc_bounds
+    ids, start, qend = HAND_BOUNDS[case]
+    ds, qe = doc_bounds(torch.tensor([ids], dtype=torch.long, device="cuda"))
+    assert ds.cpu().tolist() == [start] and qe.cpu().tolist() == [qend]
+
+
 def test_deterministic_bitwise():
     q1, k1, q2, k2, v, dout = (x.cuda() for x in gaussian_inputs(2, 3, 333, 64, 64, torch.bfloat16, 9,
                                                                  two_pairs=True))
@@ -281,17 +374,31 @@ def test_d128_bthd_layout():
     _check(compare(res, ref), BF16_FRO, BF16_MAX)
 
 
+def _grads(lib, prob, opts, dout, k1, v, H, two, q1):
+    """Gradient buffers, dpar and the plan's workspace for tnpa_x_backward with these options."""
+    from tensor_train_ing_amd import _abi
+    from tensor_train_ing_amd.poly_attn import _desc
+    bufs = {"dq1": torch.empty_like(q1), "dk1": torch.empty_like(k1), "dv": torch.empty_like(v),
+            "dq2": torch.empty_like(q1), "dk2": torch.empty_like(k1), "dpar": torch.zeros(H, 4, device="cuda")}
+    nbytes = lib.tnpa_x_workspace_bytes(ctypes.byref(prob), opts)
+    assert nbytes >= 0
+    ws = torch.empty(max(nbytes, 256), dtype=torch.uint8, device="cuda")
+    g = _abi.Grads(_desc(dout), _desc(bufs["dq1"]), _desc(bufs["dk1"]), _desc(bufs["dq2"] if two else bufs["dq1"]),
+                   _desc(bufs["dk2"] if two else bufs["dk1"]), _desc(bufs["dv"]), bufs["dpar"].data_ptr(),
+                   ws.data_ptr(), nbytes)
+    return g, bufs, ws
+
+
 @pytest.mark.parametrize("kind,dtype", [("power", torch.bfloat16), ("offset_square", torch.float16),
                                         ("lower_degree_mix", torch.bfloat16), ("power", torch.float32)])
 def test_prescaled_dout_matches_in_pass_scaling(kind, dtype):
-    """The dK/dV pass streaming the library-written row_scale * dO workspace against the pass without it. fp32 and
-    the two-pair kinds scale dO while staging it without the workspace: the same product and rounding, so
-    bit-identical gradients. 16-bit one-pair kinds at head dim 128 apply the row scale to P and H in fp32 instead (as
-    the reference does), which rounds differently: equal within 5e-3 (relative Frobenius), both within the bf16
-    tolerance of the float64 reference."""
-    import ctypes
+    """The backward streaming the library-written row_scale * dO workspace (X_PRESCALE_ON) against the backward
+    without it (X_PRESCALE_OFF). fp32 and the two-pair kinds scale dO while staging it without the workspace: the
+    same product and rounding, so bit-identical gradients. 16-bit one-pair kinds at head dim 128 apply the row scale
+    to P and H in fp32 instead (as the reference does), which rounds differently: equal within 5e-3 (relative
+    Frobenius), both within the bf16 tolerance of the float64 reference."""
     from tensor_train_ing_amd import _abi
-    from tensor_train_ing_amd.poly_attn import KINDS, _desc, _problem, _stream, doc_bounds
+    from tensor_train_ing_amd.poly_attn import KINDS, _problem, _stream, doc_bounds
     B, H, T, D = 2, 3, 300, 128 if dtype != torch.float32 else 64
     two = kind in ("signed_product", "lower_degree_mix")
     q1, k1, q2, k2, v, dout = (None if x is None else x.cuda()
@@ -307,25 +414,20 @@ def test_prescaled_dout_matches_in_pass_scaling(kind, dtype):
                     coef_f if kind == "lower_degree_mix" else None, b_f if kind == "offset_square" else None)
     lib = _abi.load()
     outs = []
-    for pre in (False, True):
-        dk1, dv, dk2 = torch.empty_like(k1), torch.empty_like(v), torch.empty_like(k1)
-        ws = torch.empty(max(1, lib.tnpa_dpar_workspace_floats(ctypes.byref(prob))), device="cuda")
-        dpar = torch.empty(H, 4, device="cuda")
-        dos = torch.empty_like(dout)
-        g = _abi.Grads(_desc(dout), _abi.Tensor(), _desc(dk1), _abi.Tensor(), _desc(dk2), _desc(dv),
-                       ws.data_ptr(), dpar.data_ptr(), _desc(dos) if pre else _abi.Tensor())
-        _abi.check(lib.tnpa_backward_phase(ctypes.byref(prob), ctypes.byref(g), _abi.PHASE_KV, _stream(q1.device)),
-                   "kv")
+    for opts in (_abi.X_PRESCALE_OFF, _abi.X_PRESCALE_ON):
+        g, bufs, ws = _grads(lib, prob, opts, dout, k1, v, H, two, q1)
+        _abi.check(lib.tnpa_x_backward(ctypes.byref(prob), ctypes.byref(g), opts, -1, _stream(q1.device)), "bwd")
         torch.cuda.synchronize()
-        outs.append((dk1, dv, dk2 if two else None, dpar if kind in ("offset_square", "lower_degree_mix") else None))
+        outs.append((bufs["dk1"], bufs["dv"], bufs["dk2"] if two else None,
+                     bufs["dpar"] if kind in ("offset_square", "lower_degree_mix") else None, bufs["dq1"]))
     ph_scaling = dtype != torch.float32 and not two  # the in-pass path scales P and H (three-buffer staging)
     if ph_scaling:
         ref = dense_reference(kind, q1, k1, q2, k2, v, dout, docs, rs, coef, bb, 2 if kind == "power" else None)
-        names = ("dk1", "dv", None, "db" if kind == "offset_square" else None)
+        names = ("dk1", "dv", None, "db" if kind == "offset_square" else None, "dq1")
     for i, (a, b2) in enumerate(zip(*outs)):
         if a is None:
             continue
-        if not ph_scaling:
+        if not ph_scaling or i == 4:  # dQ never reads the scaled dO
             assert torch.equal(a, b2)
             continue
         assert rel_fro(a, b2) < 5e-3, (i, rel_fro(a, b2))
@@ -337,37 +439,36 @@ def test_prescaled_dout_matches_in_pass_scaling(kind, dtype):
                 assert rel_fro(x, ref[name]) < BF16_FRO and rel_max(x, ref[name]) < BF16_MAX, name
 
 
-@pytest.mark.parametrize("kind", ["power", "offset_square"])
-def test_key_side_parts_equal_the_whole_pass(kind):
-    """TNPA_PHASE_KV_SCALE, then TNPA_PHASE_KV_DV and TNPA_PHASE_KV_DK as separate calls, give bit-identical dK, dV
-    and dpar to one TNPA_PHASE_KV call."""
-    import ctypes
+@pytest.mark.parametrize("kind,D,opts", [("power", 128, 1), ("offset_square", 128, 0), ("lower_degree_mix", 64, 0),
+                                         ("power", 64, 1)])
+def test_backward_launches_one_by_one_equal_the_whole_call(kind, D, opts):
+    """Each launch of the backward plan run on its own (in plan order, reading what the earlier ones wrote to the
+    workspace) gives bit-identical gradients and dpar to one whole call."""
     from tensor_train_ing_amd import _abi
-    from tensor_train_ing_amd.poly_attn import KINDS, _desc, _problem, _stream, doc_bounds
-    B, H, T, D = 2, 2, 260, 128
-    q1, k1, _, _, v, dout = (None if x is None else x.cuda()
-                             for x in gaussian_inputs(B, H, T, D, D, torch.bfloat16, 12, qk_scale=D ** -0.25))
+    from tensor_train_ing_amd.poly_attn import KINDS, _problem, _stream, doc_bounds
+    B, H, T = 2, 2, 260
+    two = kind in ("signed_product", "lower_degree_mix")
+    q1, k1, q2, k2, v, dout = (None if x is None else x.cuda() for x in gaussian_inputs(
+        B, H, T, D, D, torch.bfloat16, 12, qk_scale=D ** -0.25, two_pairs=two))
     docs = _doc_rows(B, T).cuda()
     dstart, qend = doc_bounds(docs)
     coef, bb = _params(H)
     # every tensor whose pointer goes into the problem struct stays referenced for the whole test
     rs = row_scale(docs, 1.0).float().contiguous()
-    b_f = bb.float().contiguous()
-    prob = _problem(KINDS[kind], 2, q1, k1, q1, k1, v, dstart, qend, rs, None,
-                    b_f if kind == "offset_square" else None)
+    coef_f, b_f = coef.float().contiguous(), bb.float().contiguous()
+    prob = _problem(KINDS[kind], 2, q1, k1, q2 if two else q1, k2 if two else k1, v, dstart, qend, rs,
+                    coef_f if kind == "lower_degree_mix" else None, b_f if kind == "offset_square" else None)
     lib = _abi.load()
     st = _stream(q1.device)
+    n = lib.tnpa_x_launches(ctypes.byref(prob), opts)
+    assert n >= 2
     res = []
-    for parts in ((_abi.PHASE_KV,), (_abi.PHASE_KV_SCALE, _abi.PHASE_KV_DV, _abi.PHASE_KV_DK)):
-        dk1, dv, dos = torch.empty_like(k1), torch.empty_like(v), torch.empty_like(dout)
-        ws = torch.empty(max(1, lib.tnpa_dpar_workspace_floats(ctypes.byref(prob))), device="cuda")
-        dpar = torch.zeros(H, 4, device="cuda")
-        g = _abi.Grads(_desc(dout), _abi.Tensor(), _desc(dk1), _abi.Tensor(), _desc(dk1), _desc(dv),
-                       ws.data_ptr(), dpar.data_ptr(), _desc(dos))
-        for ph in parts:
-            _abi.check(lib.tnpa_backward_phase(ctypes.byref(prob), ctypes.byref(g), ph, st), "kv part")
+    for parts in ((-1,), tuple(range(n))):
+        g, bufs, ws = _grads(lib, prob, opts, dout, k1, v, H, two, q1)
+        for i in parts:
+            _abi.check(lib.tnpa_x_backward(ctypes.byref(prob), ctypes.byref(g), opts, i, st), f"launch {i}")
         torch.cuda.synchronize()
-        res.append((dk1, dv, dpar))
+        res.append([bufs[n_] for n_ in ("dq1", "dk1", "dv", "dpar") + (("dq2", "dk2") if two else ())])
     for a, b2 in zip(*res):
         assert torch.equal(a, b2)
 
