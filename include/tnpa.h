@@ -103,6 +103,16 @@ int64_t tnpa_backward_workspace_bytes(const tnpa_problem_t* problem);
  * every reduction in a fixed order. How the work is split into kernel launches is internal to the library. */
 int tnpa_backward(const tnpa_problem_t* problem, const tnpa_grads_t* grads, void* stream);
 
+/* tnpa_backward without a caller workspace and without any device allocation, for callers that cannot allocate
+ * (code under HIP graph capture, tight serving loops, harnesses that forbid hipMalloc). No counterpart in the
+ * reference. The same results as tnpa_backward (it runs the plan that streams no row-scaled dO, bit-identical to
+ * tnpa_backward's); grads->workspace and workspace_bytes are ignored. Its scratch is a fixed 1 MiB array in each
+ * GPU's memory (the dcoef/db partials: B * H * ceil(T / 128 or 256) * 16 bytes), held until the process ends;
+ * problems that need more fail with TNPA_ERR_UNSUPPORTED before anything is enqueued. Every call on one GPU shares
+ * that GPU's array: calls that overlap on one GPU (different streams or threads) race and must be serialised by the
+ * caller. */
+int tnpa_backward_noalloc(const tnpa_problem_t* problem, const tnpa_grads_t* grads, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

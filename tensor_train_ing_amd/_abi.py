@@ -50,6 +50,7 @@ _SIGNATURES = {
     "tnpa_forward": (ctypes.c_int, [ctypes.POINTER(Problem), ctypes.POINTER(Tensor), ctypes.c_void_p]),
     "tnpa_backward_workspace_bytes": (ctypes.c_int64, [ctypes.POINTER(Problem)]),
     "tnpa_backward": (ctypes.c_int, [ctypes.POINTER(Problem), ctypes.POINTER(Grads), ctypes.c_void_p]),
+    "tnpa_backward_noalloc": (ctypes.c_int, [ctypes.POINTER(Problem), ctypes.POINTER(Grads), ctypes.c_void_p]),
 }
 # internal entry points (csrc/tnpa_internal.h): the backward's launches one by one, and its plan options
 _INTERNAL = {

@@ -5,6 +5,7 @@
 #include <cmath>
 #include <cstdarg>
 #include <cstdio>
+#include <mutex>
 #include <string>
 
 #include "../../include/tnpa.h"
@@ -454,6 +455,39 @@ int run_backward(const tnpa_problem_t* problem, const tnpa_grads_t* grads, int o
   return ok();
 }
 
+// ---------------------------------------------------------------------------------------------- static scratch
+// The workspace of tnpa_backward_noalloc: a fixed array in device memory, one copy per GPU the library runs on,
+// held until the process ends. The plan it runs (no row-scaled dO) needs scratch only for the dcoef/db partials,
+// which every call overwrites in full, so nothing in it needs clearing between calls.
+constexpr int64_t kScratchBytes = 1 << 20;
+static __device__ __align__(256) char scratch[kScratchBytes];
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxDevices] = {};
+
+// Device address of the current GPU's scratch copy, looked up once per device (the host-side name `scratch` is only a
+// stand-in and must never reach a kernel). Null on failure, with the error set.
+void* scratch_for_current_device(int* rc) {
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess || dev < 0 || dev >= kMaxDevices) {
+    *rc = fail(TNPA_ERR_LAUNCH, "tnpa_backward_noalloc: no current HIP device (%s)", hipGetErrorString(e));
+    return nullptr;
+  }
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (g_scratch_ptr[dev] == nullptr) {
+    void* ptr = nullptr;
+    e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || ptr == nullptr) {
+      *rc = fail(TNPA_ERR_LAUNCH, "tnpa_backward_noalloc: scratch address on device %d: %s", dev, hipGetErrorString(e));
+      return nullptr;
+    }
+    g_scratch_ptr[dev] = ptr;
+  }
+  return g_scratch_ptr[dev];
+}
+
 }  // namespace
 
 extern "C" {
@@ -492,6 +526,24 @@ int64_t tnpa_backward_workspace_bytes(const tnpa_problem_t* problem) { return tn
 
 int tnpa_backward(const tnpa_problem_t* problem, const tnpa_grads_t* grads, void* stream) {
   return tnpa_x_backward(problem, grads, 0, -1, stream);
+}
+
+int tnpa_backward_noalloc(const tnpa_problem_t* problem, const tnpa_grads_t* grads, void* stream) {
+  int rc = check_problem(problem);
+  if (rc) return rc;
+  if (grads == nullptr) return fail(TNPA_ERR_INVALID, "null grads");
+  Plan pl;
+  if ((rc = make_plan(*problem, TNPA_X_PRESCALE_OFF, pl))) return rc;
+  if (pl.bytes > kScratchBytes)
+    return fail(TNPA_ERR_UNSUPPORTED,
+                "tnpa_backward_noalloc: this problem needs %lld bytes of scratch, more than the %lld it holds "
+                "(use tnpa_backward with a workspace)", (long long)pl.bytes, (long long)kScratchBytes);
+  void* ptr = scratch_for_current_device(&rc);
+  if (ptr == nullptr) return rc;
+  tnpa_grads_t g = *grads;
+  g.workspace = ptr;
+  g.workspace_bytes = kScratchBytes;
+  return run_backward(problem, &g, TNPA_X_PRESCALE_OFF, -1, (hipStream_t)stream);
 }
 
 int64_t tnpa_x_workspace_bytes(const tnpa_problem_t* problem, int32_t opts) {
