@@ -228,6 +228,111 @@ def cpu_baseline(q, k, v, do, rs, degree, seconds):
                       f"fwd+bwd by autograd, median per slice, {threads} threads"}
 
 
+CE_CONFIG = {"N": 8192, "d": 2048, "V": 50304, "chunk": 4096, "seed": 7}  # pilot_1b: 4 x 2048 tokens per microbatch
+
+
+def bench_linear_ce(a):
+    """The fused linear + cross-entropy (tensor_train_ing_amd.fused_ce) at the pilot-1B unembedding shape: N tokens,
+    d_model, padded vocab, the reference's loss_chunk_tokens (ref: configs/pilot_1b.yaml:21,27,33). A step is the
+    forward and backward (bf16 matmuls, fp32 log-sum-exp). FLOPs: 8 N V d (forward GEMM; backward recompute, dX and
+    dW GEMMs). The roofline object covers this build's dominant HIP kernel, the backward epilogue, which is
+    HBM-bound: it reads and writes each chunk's bf16 logits once (4 n V bytes per launch)."""
+    import torch
+    from tensor_train_ing_amd import _abi, linear_cross_entropy_sum
+    from tensor_train_ing_amd.fused_ce import IGNORE_INDEX, _ptr, _stream
+    dev = torch.device("cuda:0")
+    c = CE_CONFIG
+    N, d, V, chunk = c["N"], c["d"], c["V"], c["chunk"]
+    g = torch.Generator().manual_seed(c["seed"])
+    x = (torch.randn(N, d, generator=g) * 0.02).to(dev, torch.bfloat16).requires_grad_()
+    w = (torch.randn(V, d, generator=g) * 0.02).to(dev, torch.bfloat16).requires_grad_()
+    t = torch.randint(0, 50257, (N,), generator=g).to(dev)
+
+    def step():
+        total = linear_cross_entropy_sum(x, w, t, chunk=chunk)
+        return torch.autograd.grad(total, (x, w))
+
+    for _ in range(a.warmup):
+        step()
+    torch.cuda.synchronize()
+    iv = event_intervals(step, a.steps)
+    ms = sum(iv) / len(iv)
+    flops = 8.0 * N * V * d
+    value = flops / (ms * 1e-3) / 1e12
+    # the epilogues alone, on one chunk of logits
+    lib = _abi.load()
+    n = chunk
+    lg = (x[:n].detach() @ w.detach().t())
+    lse = torch.empty(n, device=dev)
+    rl = torch.empty(n, device=dev)
+    tot = torch.zeros((), device=dev)
+    one = torch.ones(1, device=dev)
+    st = _stream(dev)
+    fwd_k = median_each(lambda: _abi.check(lib.tnce_forward_chunk(_ptr(lg), _abi.CE_BF16, n, V, V, _ptr(t[:n]),
+                                                                  IGNORE_INDEX, _ptr(lse), _ptr(rl), _ptr(tot), st),
+                                           "ce fwd"), a.kernel_reps)
+    work = lg.clone()
+    bwd_k = median_each(lambda: (work.copy_(lg), _abi.check(lib.tnce_backward_chunk(
+        _ptr(work), _abi.CE_BF16, n, V, V, _ptr(t[:n]), IGNORE_INDEX, _ptr(lse), _ptr(one), st), "ce bwd")),
+        a.kernel_reps)
+    copy_k = median_each(lambda: work.copy_(lg), a.kernel_reps)
+    bwd_only = max(bwd_k - copy_k, 1e-6)
+    bwd_bytes = 4.0 * n * V  # bf16 read + write
+    fwd_bytes = 2.0 * n * V
+    gemm_ms = median_each(lambda: torch.matmul(x[:n].detach(), w.detach().t(), out=lg), a.kernel_reps)
+    line = {
+        "metric": "fused linear + cross-entropy fwd+bwd TFLOP/s at the pilot-1B unembedding (N8192 d2048 V50304, "
+                  "chunk 4096, bf16)",
+        "value": round(value, 2), "unit": "TFLOP/s", "n_gpus": 1, "steps": a.steps, "warmup": a.warmup,
+        "ms_per_step": round(ms, 4), "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": "bf16", "data": "synthetic",
+        "config": {"workload": "chunked linear + cross-entropy (ref: tnlm/kernels/fused_ce.py), pilot_1b shape",
+                   **c},
+        "pct_of_peak": round(100 * value / PEAKS["bf16"], 2),
+        "kernel_ms": {"ce_forward_chunk": round(fwd_k, 4), "ce_backward_chunk": round(bwd_only, 4),
+                      "gemm_chunk_logits": round(gemm_ms, 4)},
+        "roofline": {"bound": "hbm", "kernel": "ce_backward_chunk", "achieved": round(bwd_bytes / (bwd_only * 1e-3) / 1e9, 1),
+                     "peak": 8000.0, "unit": "GB/s", "frac": round(bwd_bytes / (bwd_only * 1e-3) / 1e9 / 8000.0, 4),
+                     "traffic": None},
+        "ce_forward_chunk_gbs": round(fwd_bytes / (fwd_k * 1e-3) / 1e9, 1),
+    }
+    if not a.no_cpu_baseline:
+        line["cpu_baseline"] = ce_cpu_baseline(x, w, t, chunk, a.cpu_seconds)
+    print(json.dumps(line), flush=True)
+    return 0
+
+
+def ce_cpu_baseline(x, w, t, chunk, seconds):
+    """The CPU oracle of the fused linear + cross-entropy (oracle/fused_ce.py: numpy, float64, the reference's chunked
+    algorithm) on a bounded sample of the same rows (the full weight matrix), forward and backward; the rate is
+    scaled to the metric's FLOP convention (8 rows V d per sample)."""
+    import numpy as np
+    sys.path.insert(0, os.path.dirname(os.path.abspath(__file__)))
+    from oracle import linear_cross_entropy
+    rows = 64
+    xs = x[:rows].detach().float().cpu().numpy()
+    ws = w.detach().float().cpu().numpy()
+    ts = t[:rows].cpu().numpy()
+    done, t0 = 0, time.perf_counter()
+    while True:
+        linear_cross_entropy(xs, ws, ts, chunk=chunk)
+        done += 1
+        if time.perf_counter() - t0 >= seconds:
+            break
+    el = (time.perf_counter() - t0) / done
+    V, d = ws.shape
+    try:
+        from threadpoolctl import threadpool_info
+        threads = max([i.get("num_threads", 1) for i in threadpool_info()] or [1])
+    except Exception:
+        threads = len(os.sched_getaffinity(0))
+    return {"value": round(8.0 * rows * V * d / el / 1e12, 6), "unit": "TFLOP/s", "cores": int(threads),
+            "kind": "port", "cpu": cpu_model(),
+            "sample": f"{rows} of {x.shape[0]} rows (full {V} x {d} weight) through the CPU oracle "
+                      f"(oracle/fused_ce.py, numpy float64, forward + backward), {el * 1e3:.0f} ms per sample, "
+                      f"{done} repetitions"}
+
+
 def main(argv=None):
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -244,6 +349,9 @@ def main(argv=None):
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--kernel-reps", type=int, default=50)
+    ap.add_argument("--workload", default="attention", choices=["attention", "linear_ce"],
+                    help="attention: the headline polynomial attention step (default); linear_ce: the fused linear + "
+                         "cross-entropy at the pilot-1B unembedding shape")
     ap.add_argument("--copy-probe-mib", type=int, default=0,
                     help="only run a plain device-to-device copy of this many MiB (3 times) and exit: the known-size "
                          "kernel that calibrates rocprofv3's FETCH_SIZE / WRITE_SIZE counters")
@@ -267,6 +375,8 @@ def main(argv=None):
         print(json.dumps({"copy_probe_bytes": src.numel() * 4, "dispatches": 3}), flush=True)
         return 0
 
+    if a.workload == "linear_ce":
+        return bench_linear_ce(a)
     from tensor_train_ing_amd import poly_attention_hip
     B, H, T, D, degree, boost, seed = CONFIGS[a.config]
     kind = a.kind

@@ -19,3 +19,4 @@ from .poly_attention import (  # noqa: F401
     visible_mask,
 )
 from .torch_dense import causal_row_scale, dense_attention  # noqa: F401
+from .fused_ce import linear_cross_entropy  # noqa: F401

@@ -1,5 +1,6 @@
-"""ctypes bindings for libtnpa.so: the public C ABI (include/tnpa.h) and the internal launch-level entry points
-(csrc/tnpa_internal.h) that the benchmark and the tests use.
+"""ctypes bindings for libtnpa.so: the public C ABI (include/tnpa.h: polynomial attention; include/tnce.h: the
+fused cross-entropy epilogues) and the internal launch-level entry points (csrc/tnpa_internal.h) that the benchmark
+and the tests use.
 
 The library must be built in-tree (``python -m tensor_train_ing_amd.build``); there is no fallback: loading fails
 loudly when the shared library is missing.
@@ -16,6 +17,7 @@ ABI_VERSION = 3
 OK, ERR_INVALID, ERR_UNSUPPORTED, ERR_LAUNCH = 0, 1, 2, 3
 BF16, F32, F16 = 0, 1, 2
 SIGNED_PRODUCT, OFFSET_SQUARE, LOWER_DEGREE_MIX, POWER = 0, 1, 2, 3
+CE_BF16, CE_F32, CE_F16, CE_F64 = 0, 1, 2, 3
 
 
 class Tensor(ctypes.Structure):
@@ -41,7 +43,7 @@ class Grads(ctypes.Structure):
                 ("workspace_bytes", ctypes.c_int64)]
 
 
-# public ABI (include/tnpa.h)
+# public ABI (include/tnpa.h, include/tnce.h)
 _SIGNATURES = {
     "tnpa_abi_version": (ctypes.c_int, []),
     "tnpa_last_error": (ctypes.c_char_p, []),
@@ -51,6 +53,12 @@ _SIGNATURES = {
     "tnpa_backward_workspace_bytes": (ctypes.c_int64, [ctypes.POINTER(Problem)]),
     "tnpa_backward": (ctypes.c_int, [ctypes.POINTER(Problem), ctypes.POINTER(Grads), ctypes.c_void_p]),
     "tnpa_backward_noalloc": (ctypes.c_int, [ctypes.POINTER(Problem), ctypes.POINTER(Grads), ctypes.c_void_p]),
+    "tnce_forward_chunk": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_int32, ctypes.c_int64, ctypes.c_int64,
+                                          ctypes.c_int64, ctypes.c_void_p, ctypes.c_int64, ctypes.c_void_p,
+                                          ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p]),
+    "tnce_backward_chunk": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_int32, ctypes.c_int64, ctypes.c_int64,
+                                           ctypes.c_int64, ctypes.c_void_p, ctypes.c_int64, ctypes.c_void_p,
+                                           ctypes.c_void_p, ctypes.c_void_p]),
 }
 # internal entry points (csrc/tnpa_internal.h): the backward's launches one by one, and its plan options
 _INTERNAL = {

@@ -29,11 +29,11 @@ COMMON = [f"--offload-arch={ARCH}", "-O3", "-std=c++17", "-fPIC", "-Wall", "-Wno
 
 ELEMENT_TYPES = {"bf16": "__bf16", "f16": "_Float16", "f32": "float"}
 HEAD_DIMS = (16, 32, 64, 128)
-HEADERS = ("tnpa_device.hpp", "tnpa_kernels.hpp", "tnpa_params.hpp", "tnpa_internal.h")
+HEADERS = ("tnpa_device.hpp", "tnpa_kernels.hpp", "tnpa_params.hpp", "tnpa_internal.h", "tnpa_error.hpp")
 
 
 def _units():
-    units = [("tnpa_api", CSRC / "tnpa_api.hip", [])]
+    units = [("tnpa_api", CSRC / "tnpa_api.hip", []), ("tnce", CSRC / "tnce.hip", [])]
     for tag, ctype in ELEMENT_TYPES.items():
         for dk in HEAD_DIMS:
             units.append((f"tnpa_inst_{tag}_dk{dk}", CSRC / "tnpa_inst.hip",
@@ -44,7 +44,7 @@ def _units():
 def _stale(obj: Path, src: Path) -> bool:
     if not obj.exists():
         return True
-    deps = [src, *(CSRC / h for h in HEADERS), PKG.parent / "include" / "tnpa.h", Path(__file__)]
+    deps = [src, *(CSRC / h for h in HEADERS), *(PKG.parent / "include").glob("*.h"), Path(__file__)]
     return any(d.stat().st_mtime > obj.stat().st_mtime for d in deps)
 
 

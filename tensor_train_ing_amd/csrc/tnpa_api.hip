@@ -9,6 +9,7 @@
 #include <string>
 
 #include "../../include/tnpa.h"
+#include "tnpa_error.hpp"
 #include "tnpa_internal.h"
 #include "tnpa_params.hpp"
 
@@ -30,6 +31,23 @@ int ok() {
   g_err.clear();
   return TNPA_OK;
 }
+
+}  // namespace
+
+namespace tnpa {
+int set_error(int code, const char* fmt, ...) {
+  char buf[512];
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(buf, sizeof(buf), fmt, ap);
+  va_end(ap);
+  g_err = buf;
+  return code;
+}
+int clear_error() { return ok(); }
+}  // namespace tnpa
+
+namespace {
 
 int esize(int dtype) { return dtype == TNPA_F32 ? 4 : 2; }
 

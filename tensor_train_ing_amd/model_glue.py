@@ -45,13 +45,11 @@ def attention(kind: str, q1, k1, q2, k2, v, ctx: dict, row_power: float, coef=No
 
 
 def source_files() -> list[Path]:
-    """Every source file the operator is built from or runs: the Python package, the HIP kernels and the C ABI
-    header (the built library is excluded)."""
+    """Every source file the operators are built from or run: the Python package, the HIP kernels and the C ABI
+    headers (the built library is excluded)."""
     files = (sorted(PKG.rglob("*.py")) + sorted((PKG / "csrc").glob("*.hip")) + sorted((PKG / "csrc").glob("*.hpp"))
              + sorted((PKG / "csrc").glob("*.h")))
-    header = PKG.parent / "include" / "tnpa.h"
-    if header.exists():
-        files.append(header)
+    files += sorted((PKG.parent / "include").glob("*.h"))
     return [f for f in files if "_build" not in f.parts and "__pycache__" not in f.parts]
 
 

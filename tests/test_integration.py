@@ -63,11 +63,11 @@ def test_row_scales_match_the_visible_count():
 
 
 def test_source_identity_covers_the_kernels():
-    """Every kernel source and the C ABI header are in the identity, hashed like ref: tests/test_checkpoint.py:305."""
+    """Every kernel source and the C ABI headers are in the identity, hashed like ref: tests/test_checkpoint.py:305."""
     from tensor_train_ing_amd import model_glue
     ident = model_glue.source_sha256()
     root = model_glue.PKG.parent
-    for f in list((model_glue.PKG / "csrc").iterdir()) + [root / "include" / "tnpa.h"]:
+    for f in list((model_glue.PKG / "csrc").iterdir()) + sorted((root / "include").glob("*.h")):
         key = f.relative_to(root).as_posix()
         assert ident[key] == hashlib.sha256(f.read_bytes()).hexdigest(), key
     assert "tensor_train_ing_amd/poly_attn.py" in ident

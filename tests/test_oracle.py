@@ -313,3 +313,79 @@ def test_torch_dense_baseline_matches_oracle(kind, degree):
     for name, x in zip(("dq1", "dk1", "dq2", "dk2", "dv"), ins):
         if name in g and g[name] is not None:
             np.testing.assert_allclose(x.grad.numpy(), g[name][0, 0], rtol=1e-9, atol=1e-9)
+
+
+# ------------------------------------------------------------------ fused linear + cross-entropy oracle
+def _ce_fixture(noncontiguous=False, all_ignored=False):
+    """The reference's CPU acceptance fixture (ref: tests/test_scaling_loss.py:9-23), float64."""
+    g = torch.Generator().manual_seed(1407)
+    if noncontiguous:
+        x = torch.randn(7, 22, generator=g, dtype=torch.float64).T[::2]
+        w = torch.randn(7, 26, generator=g, dtype=torch.float64).T[::2]
+        t = torch.randint(0, 13, (22,), generator=g)[::2]
+    else:
+        x = torch.randn(11, 7, generator=g, dtype=torch.float64)
+        w = torch.randn(13, 7, generator=g, dtype=torch.float64)
+        t = torch.randint(0, 13, (11,), generator=g)
+    t = t.clone()
+    t[::3] = -100
+    if all_ignored:
+        t.fill_(-100)
+    return x, w, t
+
+
+@pytest.mark.parametrize("chunk", [1, 2, 4, 11, 30])
+@pytest.mark.parametrize("noncontiguous", [False, True])
+@pytest.mark.parametrize("scale", [1.0, -2.75, 0.0])
+def test_linear_ce_oracle_matches_dense_cross_entropy(chunk, noncontiguous, scale):
+    """The chunked oracle equals torch's dense F.cross_entropy (sum, ignore_index -100) and its autograd gradients,
+    in float64, for every chunking (ref: tests/test_scaling_loss.py:26-57)."""
+    import torch.nn.functional as F
+    from oracle import linear_cross_entropy
+    x, w, t = _ce_fixture(noncontiguous)
+    xr, wr = x.detach().clone().requires_grad_(), w.detach().clone().requires_grad_()
+    ref = F.cross_entropy(xr @ wr.T, t, ignore_index=-100, reduction="sum")
+    gx, gw = torch.autograd.grad(ref, (xr, wr), grad_outputs=torch.tensor(scale, dtype=torch.float64))
+    total, dx, dw, _ = linear_cross_entropy(x.numpy(), w.numpy(), t.numpy(), chunk=chunk, g=scale)
+    np.testing.assert_allclose(total, ref.item(), rtol=1e-12, atol=1e-12)
+    np.testing.assert_allclose(dx, gx.numpy(), rtol=1e-11, atol=1e-12)
+    np.testing.assert_allclose(dw, gw.numpy(), rtol=1e-11, atol=1e-12)
+
+
+def test_linear_ce_oracle_all_ignored_and_finite_differences():
+    from oracle import linear_cross_entropy
+    x, w, t = _ce_fixture(all_ignored=True)
+    total, dx, dw, _ = linear_cross_entropy(x.numpy(), w.numpy(), t.numpy(), chunk=4)
+    assert total == 0.0 and not dx.any() and not dw.any()
+    # central differences of the total in a few coordinates of x and w
+    x, w, t = _ce_fixture()
+    xn, wn, tn = x.numpy().copy(), w.numpy().copy(), t.numpy()
+    _, dx, dw, _ = linear_cross_entropy(xn, wn, tn, chunk=3)
+    eps = 1e-6
+    for arr, grad in ((xn, dx), (wn, dw)):
+        for idx in [(0, 0), (2, 5), (arr.shape[0] - 1, arr.shape[1] - 1)]:
+            old = arr[idx]
+            arr[idx] = old + eps
+            up = linear_cross_entropy(xn, wn, tn, chunk=3)[0]
+            arr[idx] = old - eps
+            dn = linear_cross_entropy(xn, wn, tn, chunk=3)[0]
+            arr[idx] = old
+            np.testing.assert_allclose((up - dn) / (2 * eps), grad[idx], rtol=1e-6, atol=1e-8)
+
+
+def test_linear_ce_oracle_bf16_rounding_points():
+    """With bf16 rounding the oracle stays within bf16 distance of the float64 result, and rounds exactly where the
+    reference does: its logits are bf16 values, so lse - logit[t] of a row uses those values."""
+    from oracle import linear_cross_entropy, round_to_bf16
+    rng = np.random.default_rng(5)
+    x, w = rng.standard_normal((40, 16)), rng.standard_normal((30, 16)) * 0.5
+    t = rng.integers(0, 30, 40)
+    t[::4] = -100
+    ex = linear_cross_entropy(x, w, t, chunk=7)
+    bf = linear_cross_entropy(x, w, t, chunk=7, round_to=round_to_bf16)
+    assert abs(bf[0] - ex[0]) <= 2e-2 * abs(ex[0])
+    for a, b in zip(bf[1:3], ex[1:3]):
+        assert np.abs(a - b).max() <= 3e-2 * np.abs(b).max()
+    lg = round_to_bf16(round_to_bf16(x[:7]) @ round_to_bf16(w).T)
+    m = lg.max(1, keepdims=True)
+    np.testing.assert_allclose(bf[3][:7], (m + np.log(np.exp(lg - m).sum(1, keepdims=True)))[:, 0], rtol=1e-14)
