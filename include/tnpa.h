@@ -49,7 +49,12 @@ typedef struct {
  * (offset_square, power) q2/k2 are ignored. doc_start/query_end come from tnpa_doc_bounds (ref _block_bounds,
  * tnlm/kernels/poly_attn.py:205-218, restated per token). row_scale is (B,T) fp32 contiguous: n_visible^-p for real
  * tokens, 0 for padding (ref: tnlm/kernels/poly_attn.py:312-314). coef is (H,4) fp32 contiguous for
- * lower_degree_mix; offset is (H) fp32 contiguous for offset_square. */
+ * lower_degree_mix; offset is (H) fp32 contiguous for offset_square.
+ * score_norms (optional, NULL to skip): an fp32 (pairs, 2, H) output of tnpa_forward, zero on entry, that receives
+ * max over (b, t) of the Euclidean norm of q_pair[b,h,t,:] ([pair][0][h]) and of k_pair[b,h,t,:] ([pair][1][h]),
+ * over every token (padding included), pairs = 2 for signed_product / lower_degree_mix and 1 otherwise: the two
+ * factors of the reference's Cauchy-Schwarz score bound max|S| <= max|q| max|k| / sqrt(dk)
+ * (ref: tnlm/model.py:33-38,83-85), taken from the rows the forward kernel reads anyway. */
 typedef struct {
   int32_t batch, heads, seq_len, head_dim_k, head_dim_v;
   int32_t kind;   /* tnpa_kind */
@@ -61,6 +66,7 @@ typedef struct {
   const float* row_scale;
   const float* coef;
   const float* offset;
+  float* score_norms;
 } tnpa_problem_t;
 
 /* Gradients for tnpa_backward. dout is dL/dy (B,H,T,dv). dq2/dk2 are ignored for one-pair kinds. dpar is an (H,4)

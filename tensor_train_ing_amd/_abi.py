@@ -33,7 +33,7 @@ class Problem(ctypes.Structure):
                 ("degree", ctypes.c_int32), ("dtype", ctypes.c_int32),
                 ("q1", Tensor), ("k1", Tensor), ("q2", Tensor), ("k2", Tensor), ("v", Tensor),
                 ("doc_start", ctypes.c_void_p), ("query_end", ctypes.c_void_p), ("row_scale", ctypes.c_void_p),
-                ("coef", ctypes.c_void_p), ("offset", ctypes.c_void_p)]
+                ("coef", ctypes.c_void_p), ("offset", ctypes.c_void_p), ("score_norms", ctypes.c_void_p)]
 
 
 class Grads(ctypes.Structure):

@@ -120,6 +120,7 @@ tnpa::KParams make_params(const tnpa_problem_t& p) {
   k.rscale = p.row_scale;
   k.coef = p.coef;
   k.offs = p.offset;
+  k.norms = p.score_norms;
   k.B = p.batch;
   k.H = p.heads;
   k.T = p.seq_len;

@@ -130,6 +130,28 @@ __device__ inline void poly_grad(float r1, float r2, float hg, int kind, int deg
   }
 }
 
+// Sum of squares of one operand fragment's elements in fp32.
+template <typename T> __device__ inline float op_sumsq(const typename Mfma<T>::Op& a) {
+  if constexpr (sizeof(T) == 2) {
+    float s = 0.f;
+#pragma unroll
+    for (int j = 0; j < Mfma<T>::EPL; ++j) s += (float)a[j] * (float)a[j];
+    return s;
+  } else {
+    return a * a;
+  }
+}
+
+// Score-bound factor: sumsq holds, in lanes l and l ^ 32, the two halves of one row's sum of squares (the operand
+// layout splits a row's contraction elements between the lane halves); the wave's largest row norm goes to *dst
+// with an atomic max on the float's bits (norms are >= 0, so their bit patterns order like the values).
+__device__ inline void norm_max_to(float sumsq, float* dst) {
+  float x = sqrtf(sumsq + __shfl_xor(sumsq, 32, 64));
+#pragma unroll
+  for (int o = 16; o >= 1; o >>= 1) x = fmaxf(x, __shfl_xor(x, o, 64));
+  if ((threadIdx.x & 63) == 0) atomicMax((unsigned int*)dst, __float_as_uint(x));
+}
+
 // A condition every lane of the wave evaluates identically, moved to a scalar register so the compiler branches
 // on it without exec masking.
 __device__ inline bool uniform_bool(bool c) { return __builtin_amdgcn_readfirstlane((int)c) != 0; }
@@ -276,6 +298,19 @@ k_fwd(const KParams p) {
     __syncthreads();
   }
 
+  // score-bound factor max |q|: the wave's rows are in its Q fragments
+  if (p.norms != nullptr) {
+#pragma unroll
+    for (int pr = 0; pr < NPAIR; ++pr) {
+      float ss = 0.f;
+#pragma unroll
+      for (int s = 0; s < QW; ++s)
+#pragma unroll
+        for (int c = 0; c < NCK; ++c) ss += op_sumsq<T>(qf[pr][s][c]);
+      norm_max_to(ss, p.norms + (pr * 2) * p.H + hd);
+    }
+  }
+
   f32x16 oacc[QW][NDV];
 #pragma unroll
   for (int s = 0; s < QW; ++s)
@@ -296,15 +331,25 @@ k_fwd(const KParams p) {
     for (int pr = 0; pr < NPAIR; ++pr)
 #pragma unroll
       for (int s = 0; s < QW; ++s) sacc[pr][s] = zero16();
+    // score-bound factor max |k|: every key row is the A operand of exactly one diagonal sub-block (key0 == qa[0])
+    const bool knorm = p.norms != nullptr && key0 == qa[0];
+    float kss[NPAIR];
+#pragma unroll
+    for (int pr = 0; pr < NPAIR; ++pr) kss[pr] = 0.f;
 #pragma unroll
     for (int c = 0; c < NCK; ++c)
 #pragma unroll
       for (int pr = 0; pr < NPAIR; ++pr) {
         const Op a = read_row<T, KTile>(base + pr * KTile::BYTES, 32 * kb, kappa<T>(l32), c, h);
+        if (knorm) kss[pr] += op_sumsq<T>(a);
 #pragma unroll
         for (int s = 0; s < QW; ++s)
           if (ALL || ((am >> s) & 1u)) sacc[pr][s] = M::mma(a, qf[pr][s][c], sacc[pr][s]);
       }
+    if (knorm) {
+#pragma unroll
+      for (int pr = 0; pr < NPAIR; ++pr) norm_max_to(kss[pr], p.norms + (pr * 2 + 1) * p.H + hd);
+    }
     Op pop[QW][NC2];
 #pragma unroll
     for (int s = 0; s < QW; ++s) {

@@ -29,6 +29,7 @@ struct KParams {
   const float* rscale; // (B, T) row scale n_visible^-p (0 for padding)
   const float* coef;   // (H, 4) lower_degree_mix coefficients or null
   const float* offs;   // (H) offset_square offsets or null
+  float* norms;        // (NPAIR, 2, H) max row norms of q and k (forward), or null
   float* dpar;         // (B*H, NNB, 4) per-key-block partial sums for dcoef / db, or null
   int dpre;            // 1: dsc holds the row-scaled dout; 0: the dK/dV pass scales dout while staging it
   int kvsel;           // key-side kernels to launch: 1 = dV pass, 2 = dK pass, 3 = both (or the combined kernel)

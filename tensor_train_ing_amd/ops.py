@@ -5,7 +5,8 @@ call cannot be traced, so the same HIP kernels are registered here as three opaq
 implementations and an autograd formula:
 
     tnpa::doc_bounds               (doc_ids) -> (doc_start, query_end)
-    tnpa::poly_attention           (kind, degree, q1, k1, q2?, k2?, v, doc_start, query_end, row_scale, coef?, b?) -> o
+    tnpa::poly_attention           (kind, degree, q1, k1, q2?, k2?, v, doc_start, query_end, row_scale, coef?, b?,
+                                    want_norms) -> (o, score_norms)   (score_norms empty unless want_norms)
     tnpa::poly_attention_backward  (kind, degree, q1, k1, q2?, k2?, v, doc_start, query_end, row_scale, coef?, b?, dO)
                                    -> (dq1, dk1, dq2, dk2, dv, dpar)
 
@@ -37,18 +38,24 @@ def _bounds_fake(doc_ids):
     return doc_ids.new_empty((B, T), dtype=torch.int32), doc_ids.new_empty((B, T), dtype=torch.int32)
 
 
+def _norms_shape(kind, H, want):
+    return ((2 if kind in _TWO_PAIRS else 1), 2, H) if want else (0,)
+
+
 @torch.library.custom_op("tnpa::poly_attention", mutates_args=())
 def _fwd(kind: int, degree: int, q1: torch.Tensor, k1: torch.Tensor, q2: Optional[torch.Tensor],
          k2: Optional[torch.Tensor], v: torch.Tensor, doc_start: torch.Tensor, query_end: torch.Tensor,
-         row_scale: torch.Tensor, coef: Optional[torch.Tensor], b: Optional[torch.Tensor]) -> torch.Tensor:
+         row_scale: torch.Tensor, coef: Optional[torch.Tensor], b: Optional[torch.Tensor],
+         want_norms: bool) -> tuple[torch.Tensor, torch.Tensor]:
+    norms = torch.zeros(_norms_shape(kind, q1.shape[1], want_norms), dtype=torch.float32, device=q1.device)
     o, *_ = _run_forward(kind, degree if degree > 0 else None, q1, k1, q2, k2, v, doc_start, row_scale, coef, b,
-                         out_like_v=False, bounds=(doc_start, query_end))
-    return o
+                         out_like_v=False, bounds=(doc_start, query_end), score_norms=norms if want_norms else None)
+    return o, norms
 
 
 @_fwd.register_fake
-def _fwd_fake(kind, degree, q1, k1, q2, k2, v, doc_start, query_end, row_scale, coef, b):
-    return v.new_empty(v.shape)
+def _fwd_fake(kind, degree, q1, k1, q2, k2, v, doc_start, query_end, row_scale, coef, b, want_norms):
+    return v.new_empty(v.shape), q1.new_empty(_norms_shape(kind, q1.shape[1], want_norms), dtype=torch.float32)
 
 
 @torch.library.custom_op("tnpa::poly_attention_backward", mutates_args=())
@@ -81,14 +88,14 @@ def _bwd_fake(kind, degree, q1, k1, q2, k2, v, doc_start, query_end, row_scale, 
 
 
 def _setup_context(ctx, inputs, output):
-    kind, degree, q1, k1, q2, k2, v, dstart, qend, row_scale, coef, b = inputs
+    kind, degree, q1, k1, q2, k2, v, dstart, qend, row_scale, coef, b, _want = inputs
     ctx.kind, ctx.degree = kind, degree
     ctx.coef_dtype = coef.dtype if coef is not None else None
     ctx.b_dtype = b.dtype if b is not None else None
     ctx.save_for_backward(q1, k1, q2, k2, v, dstart, qend, row_scale, coef, b)
 
 
-def _backward(ctx, do):
+def _backward(ctx, do, _dnorms):
     q1, k1, q2, k2, v, dstart, qend, row_scale, coef, b = ctx.saved_tensors
     kind = ctx.kind
     dq1, dk1, dq2, dk2, dv, dpar = _bwd(kind, ctx.degree, q1, k1, q2, k2, v, dstart, qend, row_scale, coef, b,
@@ -96,18 +103,22 @@ def _backward(ctx, do):
     two = kind in _TWO_PAIRS
     dcoef = dpar.to(ctx.coef_dtype) if (kind == _abi.LOWER_DEGREE_MIX and coef is not None) else None
     db = dpar[:, 0].to(ctx.b_dtype) if (kind == _abi.OFFSET_SQUARE and b is not None) else None
-    return (None, None, dq1, dk1, dq2 if two else None, dk2 if two else None, dv, None, None, None, dcoef, db)
+    return (None, None, dq1, dk1, dq2 if two else None, dk2 if two else None, dv, None, None, None, dcoef, db, None)
 
 
 _fwd.register_autograd(_backward, setup_context=_setup_context)
 
 
-def poly_attention_op(kind, q1, k1, q2, k2, v, doc_ids, row_scale, coef=None, b=None, *, degree=None, bounds=None):
+def poly_attention_op(kind, q1, k1, q2, k2, v, doc_ids, row_scale, coef=None, b=None, *, degree=None, bounds=None,
+                      score_norms=None):
     """poly_attention_hip through the registered custom ops (same arguments, same results; contiguous output).
     Unknown kinds raise KeyError, as the reference."""
     K, degree = _canonical(kind, q1, k1, q2, k2, degree)
     two = K in _TWO_PAIRS
     dstart, qend = doc_bounds_op(doc_ids) if bounds is None else bounds
-    return _fwd(K, int(degree) if degree is not None else 0, q1, k1, q2 if two else None, k2 if two else None,
-                v, dstart, qend, row_scale, coef if K == _abi.LOWER_DEGREE_MIX else None,
-                b if K == _abi.OFFSET_SQUARE else None)
+    o, norms = _fwd(K, int(degree) if degree is not None else 0, q1, k1, q2 if two else None, k2 if two else None,
+                    v, dstart, qend, row_scale, coef if K == _abi.LOWER_DEGREE_MIX else None,
+                    b if K == _abi.OFFSET_SQUARE else None, score_norms is not None)
+    if score_norms is not None:
+        score_norms.copy_(torch.maximum(score_norms, norms))
+    return o

@@ -138,7 +138,8 @@ def _check_bounds(bounds, doc_ids):
     return bounds[0], bounds[1]
 
 
-def _run_forward(K, degree, q1, k1, q2, k2, v, doc_ids, row_scale, coef, b, out_like_v=True, bounds=None):
+def _run_forward(K, degree, q1, k1, q2, k2, v, doc_ids, row_scale, coef, b, out_like_v=True, bounds=None,
+                 score_norms=None):
     """Validates, computes the document bounds (unless given) and launches the forward. Returns (o, dstart, qend,
     (q1, k1, q2, k2, v) as the kernels read them, sc, coef_f, b_f). o has v's strides (out_like_v) or is
     contiguous."""
@@ -155,7 +156,12 @@ def _run_forward(K, degree, q1, k1, q2, k2, v, doc_ids, row_scale, coef, b, out_
     o = torch.empty_like(v) if out_like_v else None
     if o is None or not _aligned_rows(o):
         o = torch.empty(v.shape, dtype=v.dtype, device=v.device)
-    prob = _problem(K, degree, q1, k1, q2, k2, v, dstart, qend, sc, coef_f, b_f)
+    if score_norms is not None:
+        pairs = 2 if K in _TWO_PAIRS else 1
+        if (score_norms.dtype != torch.float32 or tuple(score_norms.shape) != (pairs, 2, q1.shape[1])
+                or not score_norms.is_contiguous() or score_norms.device != q1.device):
+            raise ValueError(f"score_norms must be a contiguous float32 ({pairs}, 2, H) tensor on q1's device")
+    prob = _problem(K, degree, q1, k1, q2, k2, v, dstart, qend, sc, coef_f, b_f, score_norms)
     lib = _abi.load()
     with torch.cuda.device(q1.device):
         _abi.check(lib.tnpa_forward(ctypes.byref(prob), ctypes.byref(_desc(o)), _stream(q1.device)),
@@ -195,11 +201,12 @@ class PolyAttention(torch.autograd.Function):
     """ref: tnlm/kernels/poly_attn.py:255-309, with an appended `degree` argument for kind="power"."""
 
     @staticmethod
-    def forward(ctx, kind, q1, k1, q2, k2, v, doc_ids, row_scale, coef, b, degree=None, bounds=None):
+    def forward(ctx, kind, q1, k1, q2, k2, v, doc_ids, row_scale, coef, b, degree=None, bounds=None,
+                score_norms=None):
         shared = KINDS[kind] == _abi.SIGNED_PRODUCT and q2 is q1 and k2 is k1
         K, degree = _canonical(kind, q1, k1, q2, k2, degree)
         o, dstart, qend, (q1, k1, q2, k2, v), sc, coef_f, b_f = _run_forward(
-            K, degree, q1, k1, q2, k2, v, doc_ids, row_scale, coef, b, bounds=bounds)
+            K, degree, q1, k1, q2, k2, v, doc_ids, row_scale, coef, b, bounds=bounds, score_norms=score_norms)
         ctx.save_for_backward(q1, k1, q2, k2, v, dstart, qend, sc, coef_f, b_f)
         ctx.K, ctx.degree, ctx.shared = K, degree, shared
         ctx.has_coef, ctx.has_b = coef is not None, b is not None
@@ -215,7 +222,7 @@ class PolyAttention(torch.autograd.Function):
                                                       b_f, do)
         dcoef = dpar.to(ctx.coef_dtype) if (K == _abi.LOWER_DEGREE_MIX and ctx.has_coef) else None
         db = dpar[:, 0].to(ctx.b_dtype) if (K == _abi.OFFSET_SQUARE and ctx.has_b) else None
-        return None, dq1, dk1, dq2, dk2, dv, None, None, dcoef, db, None, None
+        return None, dq1, dk1, dq2, dk2, dv, None, None, dcoef, db, None, None, None
 
 
 def _alloc_like(x: torch.Tensor) -> torch.Tensor:
@@ -223,23 +230,41 @@ def _alloc_like(x: torch.Tensor) -> torch.Tensor:
     return y if _aligned_rows(y) else torch.empty(x.shape, dtype=x.dtype, device=x.device)
 
 
-def _problem(K, degree, q1, k1, q2, k2, v, dstart, qend, sc, coef_f, b_f) -> _abi.Problem:
+def _problem(K, degree, q1, k1, q2, k2, v, dstart, qend, sc, coef_f, b_f, score_norms=None) -> _abi.Problem:
     B, H, T, DK = q1.shape
     return _abi.Problem(B, H, T, DK, v.shape[-1], K, int(degree) if degree is not None else 0, _DTYPES[q1.dtype],
                         _desc(q1), _desc(k1), _desc(q2), _desc(k2), _desc(v),
                         dstart.data_ptr(), qend.data_ptr(), sc.data_ptr(),
                         coef_f.data_ptr() if coef_f is not None else None,
-                        b_f.data_ptr() if b_f is not None else None)
+                        b_f.data_ptr() if b_f is not None else None,
+                        score_norms.data_ptr() if score_norms is not None else None)
+
+
+def score_norm_buffer(kind, q1, k1, q2=None, k2=None) -> torch.Tensor:
+    """A zeroed fp32 (pairs, 2, H) buffer for the forward's score-bound factors: pairs = 2 for the two-pair kinds,
+    1 for the others and for signed_product with shared pairs (which runs as degree 2)."""
+    K, _ = _canonical(kind, q1, k1, q2, k2, 2)
+    return torch.zeros(2 if K in _TWO_PAIRS else 1, 2, q1.shape[1], dtype=torch.float32, device=q1.device)
+
+
+def score_bound(score_norms: torch.Tensor, d_key: int) -> dict:
+    """{"S1": (H,), ["S2": (H,)]} = max|q| * max|k| / sqrt(dk) per head from the forward's score_norms: the reference's
+    Cauchy-Schwarz bound on max |S| (ref: tnlm/model.py:33-38), without a separate pass over q and k."""
+    names = ("S1", "S2")
+    return {names[i]: score_norms[i, 0] * score_norms[i, 1] / d_key ** 0.5 for i in range(score_norms.shape[0])}
 
 
 def poly_attention_hip(kind, q1, k1, q2, k2, v, doc_ids, row_scale, coef=None, b=None, *, degree=None,
-                       bounds=None):
+                       bounds=None, score_norms=None):
     """q*, k*: (B, H, T, dk); v: (B, H, T, dv); doc_ids: (B, T) contiguous ids, < 0 = padding;
     row_scale: (B, T) = n_visible^-p for real queries, 0 for padding. kind="power" takes degree=p and ignores
-    q2/k2. bounds: optional doc_bounds(doc_ids), computed once per batch by a caller with many layers. Every
-    gradient is reduced in a fixed order (deterministic).  ref: tnlm/kernels/poly_attn.py:312-315"""
+    q2/k2. bounds: optional doc_bounds(doc_ids), computed once per batch by a caller with many layers.
+    score_norms: optional zeroed float32 (pairs, 2, H) tensor (score_norm_buffer) that the forward fills with the
+    per-head max |q| and max |k| of each pair, for score_bound(). Every gradient is reduced in a fixed order
+    (deterministic).  ref: tnlm/kernels/poly_attn.py:312-315"""
     if torch.compiler.is_compiling():
         # under torch.compile the same kernels run behind registered custom ops (opaque to the compiler)
         from .ops import poly_attention_op
-        return poly_attention_op(kind, q1, k1, q2, k2, v, doc_ids, row_scale, coef, b, degree=degree, bounds=bounds)
-    return PolyAttention.apply(kind, q1, k1, q2, k2, v, doc_ids, row_scale, coef, b, degree, bounds)
+        return poly_attention_op(kind, q1, k1, q2, k2, v, doc_ids, row_scale, coef, b, degree=degree, bounds=bounds,
+                                 score_norms=score_norms)
+    return PolyAttention.apply(kind, q1, k1, q2, k2, v, doc_ids, row_scale, coef, b, degree, bounds, score_norms)

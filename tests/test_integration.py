@@ -17,8 +17,8 @@ def test_custom_ops_are_registered_with_the_reference_argument_order():
     bwd = str(torch.ops.tnpa.poly_attention_backward.default._schema)
     bounds = str(torch.ops.tnpa.doc_bounds.default._schema)
     assert "Tensor q1, Tensor k1, Tensor? q2, Tensor? k2, Tensor v, Tensor doc_start, Tensor query_end, " \
-           "Tensor row_scale, Tensor? coef, Tensor? b" in fwd
-    assert fwd.endswith("-> Tensor")
+           "Tensor row_scale, Tensor? coef, Tensor? b, bool want_norms" in fwd
+    assert fwd.endswith("-> (Tensor, Tensor)")
     assert "Tensor doc_ids" in bounds and bounds.endswith("-> (Tensor, Tensor)")
     assert "Tensor dout" in bwd and bwd.endswith("-> (Tensor, Tensor, Tensor, Tensor, Tensor, Tensor)")
 
@@ -35,8 +35,9 @@ def test_fake_shapes(kind, two, par):
         rs = torch.ones(2, 40)
         ds, qe = torch.ops.tnpa.doc_bounds(doc)
         assert ds.shape == qe.shape == (2, 40) and ds.dtype == torch.int32
-        o = torch.ops.tnpa.poly_attention(kind, 2, q, q, q if two else None, q if two else None, v, ds, qe, rs,
-                                          None, None)
+        o, nrm = torch.ops.tnpa.poly_attention(kind, 2, q, q, q if two else None, q if two else None, v, ds, qe, rs,
+                                               None, None, True)
+        assert tuple(nrm.shape) == ((2 if two else 1), 2, 3) and nrm.dtype == torch.float32
         assert o.shape == v.shape and o.dtype == v.dtype and o.is_contiguous()
         g = torch.ops.tnpa.poly_attention_backward(kind, 2, q, q, q if two else None, q if two else None, v, ds, qe,
                                                    rs, None, None, v)

@@ -526,3 +526,43 @@ def test_doc_bounds_match_oracle(T, dtype):
     rs, rq = oracle_bounds(wide[:, :T].numpy())
     np.testing.assert_array_equal(ds.cpu().numpy(), rs)
     np.testing.assert_array_equal(qe.cpu().numpy(), rq)
+
+
+# ------------------------------------------------------------------ score-bound factors from the forward kernel
+@pytest.mark.parametrize("kind,B,H,T,D,dtype", [
+    ("power", 2, 3, 300, 128, torch.bfloat16), ("power", 1, 2, 1000, 64, torch.bfloat16),
+    ("signed_product", 2, 2, 260, 128, torch.bfloat16), ("lower_degree_mix", 1, 3, 200, 64, torch.float16),
+    ("offset_square", 2, 2, 150, 32, torch.float32), ("signed_product", 1, 2, 77, 16, torch.float32)])
+def test_forward_score_norms_equal_the_reference_bound(kind, B, H, T, D, dtype):
+    """The forward kernel's per-head max |q| and max |k| (every token, padding included) equal the reference's
+    score_bound factors q.float().norm(-1).amax((0, 2)) (ref: tnlm/model.py:33-38) to float32 rounding, with
+    documents, padding and a ragged last block; the attention output is unchanged by asking for them."""
+    from tensor_train_ing_amd import poly_attention_hip, score_bound, score_norm_buffer
+    print(f"[score norms] {kind} B{B} H{H} T{T} D{D} {dtype}", flush=True)
+    two = kind in ("signed_product", "lower_degree_mix")
+    q1, k1, q2, k2, v, _ = (None if x is None else x.cuda() for x in gaussian_inputs(
+        B, H, T, D, D, dtype, 31, qk_scale=D ** -0.25, boost_rows=0.02, two_pairs=two, layout="bthd"))
+    doc = _doc_rows(B, T).cuda() if T >= 100 else torch.zeros(B, T, dtype=torch.long, device="cuda")
+    rs = row_scale(doc, 0.5)
+    coef, bb = _params(H)
+    kw = dict(coef=coef if kind == "lower_degree_mix" else None, b=bb if kind == "offset_square" else None,
+              degree=2 if kind == "power" else None)
+    norms = score_norm_buffer(kind, q1, k1, q2, k2)
+    with torch.no_grad():
+        o1 = poly_attention_hip(kind, q1, k1, q2, k2, v, doc, rs, score_norms=norms, **kw)
+        o2 = poly_attention_hip(kind, q1, k1, q2, k2, v, doc, rs, **kw)
+    assert torch.equal(o1, o2)
+    pairs = [(q1, k1)] + ([(q2, k2)] if two else [])
+    for i, (q, k) in enumerate(pairs):
+        for j, x in enumerate((q, k)):
+            ref = x.float().norm(dim=-1).amax(dim=(0, 2))
+            torch.testing.assert_close(norms[i, j], ref, rtol=2e-6, atol=0)
+    sb = score_bound(norms, D)
+    ref_s1 = q1.float().norm(dim=-1).amax(dim=(0, 2)) * k1.float().norm(dim=-1).amax(dim=(0, 2)) / D ** 0.5
+    torch.testing.assert_close(sb["S1"], ref_s1, rtol=5e-6, atol=0)
+    # the custom-op path (what torch.compile traces) returns the same factors
+    from tensor_train_ing_amd import poly_attention_op
+    n2 = score_norm_buffer(kind, q1, k1, q2, k2)
+    with torch.no_grad():
+        o3 = poly_attention_op(kind, q1, k1, q2, k2, v, doc, rs, score_norms=n2, **kw)
+    assert torch.equal(o3, o1.contiguous()) and torch.equal(n2, norms)
