@@ -44,9 +44,10 @@ CONFIGS = {  # name: (B, H, T, D, degree, boost_rows, seed) -- BASELINE.json con
     "7b": (2, 32, 4096, 128, 2, 0.0, 4),
 }
 # matrix units (of 2*B*H*Npairs*D FLOP) each launch executes: fwd QK^T + PV; dv pass S + dV; dk pass S + dP + dK;
-# combined key side S + dP + dV + dK; dq pass S + dP + dQ; with two pairs one more S, dK and dQ each. The dO
-# row-scaling pass and the dpar reduction are bandwidth kernels with no matrix work.
-UNITS_ONE = {"fwd": 2, "dv": 2, "dk": 3, "kv": 4, "q": 3, "scale": 0, "dpar": 0}
+# combined key side S + dP + dV + dK; dq pass S + dP + dQ; dQ from the stored dS tiles (qds) dQ only; with two
+# pairs one more S, dK and dQ each. The dO row-scaling pass and the dpar reduction are bandwidth kernels with no
+# matrix work.
+UNITS_ONE = {"fwd": 2, "dv": 2, "dk": 3, "kv": 4, "q": 3, "qds": 1, "scale": 0, "dpar": 0}
 UNITS_TWO = {"fwd": 3, "kv": 6, "q": 5, "scale": 0, "dpar": 0}
 
 

@@ -68,7 +68,7 @@ _INTERNAL = {
     "tnpa_x_backward": (ctypes.c_int, [ctypes.POINTER(Problem), ctypes.POINTER(Grads), ctypes.c_int32, ctypes.c_int32,
                                        ctypes.c_void_p]),
 }
-X_PRESCALE_ON, X_PRESCALE_OFF = 1, 2
+X_PRESCALE_ON, X_PRESCALE_OFF, X_DS_OFF = 1, 2, 4
 
 _LIB = None
 

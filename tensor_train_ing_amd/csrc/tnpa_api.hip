@@ -359,25 +359,31 @@ __global__ void k_dpar_reduce(const float* part, int B, int H, int NNB, float* o
 // ---------------------------------------------------------------------------------------------- backward plan
 // The launches of one backward call and the carving of the caller's workspace:
 //   scale  row_scale * dO into the workspace (where the key side cannot scale dO for free, or when forced)
-//   kv     the combined dK/dV kernel, or dv and dk: the two passes of the split key side (16-bit, one q/k pair,
-//          head dim above 64)
-//   q      the dQ kernel
+//   kv     the combined dK/dV kernel (the wave-pair kernel for 16-bit, one q/k pair, head dims 128), or dv and
+//          dk: the two passes of the split key side (16-bit, one q/k pair, other head dims above 64)
+//   q      the dQ kernel (recomputes S and dP)
+//   qds    dQ = dS K from the dS tiles the dk pass stored in the workspace (16-bit, one q/k pair, head dim 128,
+//          unless TNPA_X_DS_OFF or the tiles would exceed kMaxDsTileBytes): one matrix product instead of three
 //   dpar   the fixed-order dcoef/db reduction of the per-key-block partials (offset_square, lower_degree_mix)
-enum LaunchKind { L_SCALE = 0, L_KV = 1, L_DV = 2, L_DK = 3, L_Q = 4, L_DPAR = 5 };
-const char* const kLaunchNames[] = {"scale", "kv", "dv", "dk", "q", "dpar"};
+enum LaunchKind { L_SCALE = 0, L_KV = 1, L_DV = 2, L_DK = 3, L_Q = 4, L_DPAR = 5, L_QDS = 6 };
+const char* const kLaunchNames[] = {"scale", "kv", "dv", "dk", "q", "dpar", "qds"};
+
+// Largest dS tile area the plan uses (B * H * T^2 bytes for 16-bit inputs, 545 MB at B8 H16 T2048); larger problems
+// recompute S and dP in the dQ kernel instead.
+constexpr int64_t kMaxDsTileBytes = 4LL << 30;
 
 struct Plan {
   int n = 0;
   int what[6] = {0, 0, 0, 0, 0, 0};
-  bool prescale = false, par = false;
+  bool prescale = false, par = false, ds = false;
   int nnb = 0;  // key blocks per row (dpar partials)
-  int64_t dpar_off = 0, dos_off = 0, bytes = 0;
+  int64_t dpar_off = 0, dos_off = 0, ds_off = 0, bytes = 0;
 };
 
 int64_t align256(int64_t x) { return (x + 255) & ~(int64_t)255; }
 
 int make_plan(const tnpa_problem_t& p, int opts, Plan& pl) {
-  if ((opts & ~(TNPA_X_PRESCALE_ON | TNPA_X_PRESCALE_OFF)) != 0 ||
+  if ((opts & ~(TNPA_X_PRESCALE_ON | TNPA_X_PRESCALE_OFF | TNPA_X_DS_OFF)) != 0 ||
       (opts & (TNPA_X_PRESCALE_ON | TNPA_X_PRESCALE_OFF)) == (TNPA_X_PRESCALE_ON | TNPA_X_PRESCALE_OFF))
     return fail(TNPA_ERR_INVALID, "invalid backward options %d", opts);
   const bool f32 = p.dtype == TNPA_F32;
@@ -391,17 +397,20 @@ int make_plan(const tnpa_problem_t& p, int opts, Plan& pl) {
   pl.nnb = (p.seq_len + bk - 1) / bk;
   const int64_t dpar_bytes = pl.par ? (int64_t)p.batch * p.heads * pl.nnb * 4 * (int64_t)sizeof(float) : 0;
   const int64_t dos_bytes = pl.prescale ? (int64_t)p.batch * p.heads * p.seq_len * dv * esize(p.dtype) : 0;
+  const int64_t ds_bytes = tnpa::ds_tile_bytes(p.batch, p.heads, p.seq_len, esize(p.dtype));
+  pl.ds = split && !f32 && dk == 128 && !(opts & TNPA_X_DS_OFF) && ds_bytes <= kMaxDsTileBytes;
   pl.dpar_off = 0;
   pl.dos_off = align256(dpar_bytes);
-  pl.bytes = pl.prescale ? pl.dos_off + align256(dos_bytes) : align256(dpar_bytes);
+  pl.ds_off = pl.dos_off + align256(dos_bytes);
+  pl.bytes = pl.ds_off + (pl.ds ? align256(ds_bytes) : 0);
   if (pl.prescale) pl.what[pl.n++] = L_SCALE;
-  if (split) {
+  if (split && !tnpa::kv_pair(f32, poly, dk, dv)) {
     pl.what[pl.n++] = L_DV;
     pl.what[pl.n++] = L_DK;
   } else {
     pl.what[pl.n++] = L_KV;
   }
-  pl.what[pl.n++] = L_Q;
+  pl.what[pl.n++] = pl.ds ? L_QDS : L_Q;
   if (pl.par) pl.what[pl.n++] = L_DPAR;
   return TNPA_OK;
 }
@@ -445,6 +454,7 @@ int run_backward(const tnpa_problem_t* problem, const tnpa_grads_t* grads, int o
     k.dsc = desc(dos);
     k.dpre = 1;
   }
+  if (pl.ds) k.dstile = ws + pl.ds_off;
   for (int i = 0; i < pl.n; ++i) {
     if (only != -1 && i != only) continue;
     hipError_t e = hipSuccess;
@@ -460,6 +470,10 @@ int run_backward(const tnpa_problem_t* problem, const tnpa_grads_t* grads, int o
       case L_DV: k.kvsel = 1; e = run(PH_BWD_KV, p, k, stream); break;
       case L_DK: k.kvsel = 2; e = run(PH_BWD_KV, p, k, stream); break;
       case L_Q: e = run(PH_BWD_Q, p, k, stream); break;
+      case L_QDS:
+        e = p.dtype == TNPA_BF16 ? tnpa::launch_bwd_q_ds<__bf16, 128>(k, stream)
+                                 : tnpa::launch_bwd_q_ds<_Float16, 128>(k, stream);
+        break;
       case L_DPAR: {
         const int n = p.heads * 4;
         hipLaunchKernelGGL(k_dpar_reduce, dim3((n + 255) / 256), dim3(256), 0, stream, (const float*)k.dpar, p.batch,
@@ -552,7 +566,7 @@ int tnpa_backward_noalloc(const tnpa_problem_t* problem, const tnpa_grads_t* gra
   if (rc) return rc;
   if (grads == nullptr) return fail(TNPA_ERR_INVALID, "null grads");
   Plan pl;
-  if ((rc = make_plan(*problem, TNPA_X_PRESCALE_OFF, pl))) return rc;
+  if ((rc = make_plan(*problem, TNPA_X_PRESCALE_OFF | TNPA_X_DS_OFF, pl))) return rc;
   if (pl.bytes > kScratchBytes)
     return fail(TNPA_ERR_UNSUPPORTED,
                 "tnpa_backward_noalloc: this problem needs %lld bytes of scratch, more than the %lld it holds "
@@ -562,7 +576,7 @@ int tnpa_backward_noalloc(const tnpa_problem_t* problem, const tnpa_grads_t* gra
   tnpa_grads_t g = *grads;
   g.workspace = ptr;
   g.workspace_bytes = kScratchBytes;
-  return run_backward(problem, &g, TNPA_X_PRESCALE_OFF, -1, (hipStream_t)stream);
+  return run_backward(problem, &g, TNPA_X_PRESCALE_OFF | TNPA_X_DS_OFF, -1, (hipStream_t)stream);
 }
 
 int64_t tnpa_x_workspace_bytes(const tnpa_problem_t* problem, int32_t opts) {

@@ -22,4 +22,5 @@ TNPA_INST_DVS(POLY_POW2)
 TNPA_INST_DVS(POLY_POW4)
 TNPA_INST_DVS(POLY_OS)
 TNPA_INST_DVS(POLY_SP)
+template hipError_t launch_bwd_q_ds<TNPA_INST_T, TNPA_INST_DK>(const KParams&, hipStream_t);
 }  // namespace tnpa

@@ -19,6 +19,7 @@ extern "C" {
 /* Options of the backward plan. 0 is what tnpa_backward runs. */
 #define TNPA_X_PRESCALE_ON 1  /* write row_scale * dO into the workspace first and stream it (where the plan would not) */
 #define TNPA_X_PRESCALE_OFF 2 /* never write it: the dK/dV kernels apply the row scale themselves */
+#define TNPA_X_DS_OFF 4       /* dQ recomputes S and dP (no dS tiles in the workspace) where the plan would read dS */
 
 /* Workspace bytes of the backward plan with these options (-1 for an invalid problem or options). */
 int64_t tnpa_x_workspace_bytes(const tnpa_problem_t* problem, int32_t opts);
@@ -26,7 +27,7 @@ int64_t tnpa_x_workspace_bytes(const tnpa_problem_t* problem, int32_t opts);
 /* Number of kernel launches of the plan (-1 for an invalid problem or options). */
 int32_t tnpa_x_launches(const tnpa_problem_t* problem, int32_t opts);
 
-/* Short name of launch i of the plan ("scale", "kv", "dv", "dk", "q", "dpar"), or "" when i is out of range. */
+/* Short name of launch i of the plan ("scale", "kv", "dv", "dk", "q", "qds", "dpar"), or "" when i is out of range. */
 const char* tnpa_x_launch_name(const tnpa_problem_t* problem, int32_t opts, int32_t i);
 
 /* Runs the plan's launches (only = -1) or launch `only` alone; a launch run alone reads what the launches before it

@@ -1155,6 +1155,21 @@ k_bwd_kv(const KParams p) {
         }
       }
     }
+    // the dK pass of a one-pair 16-bit kind also stores dS for the dQ-from-dS kernel: tile (query sub-block,
+    // key sub-block), each of its two operands one contiguous KiB (layout at ds_tile_rows)
+    if constexpr (MODE == KV_DK && NPAIR == 1 && sizeof(T) == 2) {
+      if (p.dstile != nullptr) {
+        const int qi = (m >> 5) + qb;
+        T* tb = (T*)p.dstile + ((int64_t)bh * ds_tiles_per_head(T_) + (int64_t)qi * (qi + 1) / 2) * 1024 + l32 * 16 + h * 8;
+#pragma unroll
+        for (int s = 0; s < KW; ++s) {
+          if (!(ALL || ((am >> s) & 1u))) continue;
+          T* tp = tb + (int64_t)(ka[s] >> 5) * 1024;
+#pragma unroll
+          for (int c2 = 0; c2 < NC2; ++c2) __builtin_nontemporal_store(dso[0][s][c2], (Op*)(tp + 512 * c2));
+        }
+      }
+    }
     if constexpr (WANT_DV) {
 #pragma unroll
       for (int d = 0; d < NDV; ++d)
@@ -1344,6 +1359,456 @@ k_bwd_kv(const KParams p) {
   }
 }
 
+// ------------------------------------------------------------------------------------------------ dK / dV, wave pairs
+// ref: tnlm/kernels/poly_attn.py:77-148 (_bwd_kv), for 16-bit inputs, one q/k pair, head dim 128. S and dP are computed
+// once per (query, key) sub-block, by splitting the work of 32 keys between two waves on one SIMD by product rather
+// than by rows (each role then holds half the state, so both fit two waves per SIMD):
+//   producer (waves 0-3): the K and V rows of its 32 keys in registers; per 32-query sub-block S = Q K^T and
+//            dP = dO V^T from LDS row reads of the staged Q / dO tile; P = mask(A(S)) * row_scale and
+//            dS = mask(A'(S) * dP * row_scale) in fp32 (ref: tnlm/kernels/poly_attn.py:113-136), each rounded to the
+//            input dtype into the pair's exchange slot in LDS (and dS into the dS tiles when dQ is read from them);
+//   consumer (waves 4-7): one sub-block behind, dV^T += dO^T P and dK^T += Q^T dS from transposed reads of the same
+//            staged tiles, the dV and dK accumulators in registers. The consumers also stage the Q / dO tiles, so
+//            the producers' global stores never sit ahead of a load somebody waits for (loads and stores retire in
+//            issue order).
+// A workgroup owns 128 keys (pair p: keys n0 + 32 p .. + 31; waves p and p + 4 share SIMD p). One barrier per 32-query
+// step publishes the exchange slot and the staged tiles: step k runs producer sub-block k and consumer sub-block k-1.
+// Per sub-block and pair 16 + 16 matrix instructions, against 16 + 24 for the separate dV and dK passes. The rounding
+// points are those of the passes, so dK and dV are bit-identical to theirs.
+template <typename T, int POLY, int DK, int DV>
+__global__ void __attribute__((amdgpu_flat_work_group_size(512, 512), amdgpu_waves_per_eu(2)))
+k_bwd_kv_pair(const KParams p) {
+  typedef Mfma<T> M;
+  typedef typename M::Op Op;
+  static_assert(sizeof(T) == 2 && !two_pair_poly(POLY) && DK == 128 && DV == 128, "16-bit, one pair, head dim 128");
+  constexpr int KC = M::KC, EPL = M::EPL;
+  constexpr bool PRE = prescaled<T, POLY>();
+  constexpr bool PAR = POLY == POLY_OS;
+  constexpr int NCK = DK / KC, NCV = DV / KC, NDK = DK / 32, NDV = DV / 32, NC2 = 32 / KC;
+  constexpr int NPR = 4, BNK = 32 * NPR, BMQ = 64;
+  typedef Tile<T, BMQ, DK> QTile;
+  typedef Tile<T, BMQ, DV> OTile;
+  typedef Tile<T, BNK, DK> KRows;
+  typedef Tile<T, BNK, DV> VRows;
+  constexpr int DSOFF = QTile::BYTES + OTile::BYTES;  // per query of the tile: doc start (int), row scale (float)
+  constexpr int BUF = DSOFF + BMQ * 8;
+  constexpr int NBUF = 3;
+  constexpr int XSLOT = 2 * NC2 * 64 * 16;  // P and dS operands of one sub-block, 16 bytes per lane each
+  constexpr int XOFF = NBUF * BUF;
+  constexpr int SMEM = cmax(XOFF + NPR * 2 * XSLOT, KRows::BYTES + VRows::BYTES);
+  static_assert(SMEM <= 160 * 1024 - 64, "LDS");
+  __shared__ __attribute__((aligned(16))) char smem_[SMEM];
+  __shared__ float red_[NPR][4];
+  char TNPA_LDS* smem = (char TNPA_LDS*)smem_;
+
+  const int T_ = p.T, BH = p.B * p.H;
+  const int NNB = (T_ + BNK - 1) / BNK;
+  const int item = blockIdx.x;
+  const int nb = item / BH, bh = item % BH, b = bh / p.H, hd = bh % p.H;
+  const int n0 = nb * BNK;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, h = lane >> 5, l32 = lane & 31;
+  const bool prod = wave < NPR;
+  const int pr = wave & (NPR - 1);
+  const int ka = n0 + 32 * pr;
+  const T* qp = head_ptr<T>(p.q1, b, hd);
+  const T* kp = head_ptr<T>(p.k1, b, hd);
+  const T* vp = head_ptr<T>(p.v, b, hd);
+  const T* dop = p.dpre ? head_ptr<T>(p.dsc, b, hd) : head_ptr<T>(p.dout, b, hd);
+  const int64_t dost = p.dpre ? p.dsc.st : p.dout.st;
+  const Coefs cf = load_coefs(p, hd);
+  const int* dst = p.dstart + (int64_t)b * T_;
+  const float* rsc = p.rscale + (int64_t)b * T_;
+
+  // K and V rows of the block through LDS as whole rows (every thread); the producers take their operands from there
+  {
+    Stage<T, BNK, DK, DK, 512> ks;
+    Stage<T, BNK, DV, DV, 512> vs;
+    ks.load(kp, p.k1.st, n0, T_ - n0);
+    vs.load(vp, p.v.st, n0, T_ - n0);
+    ks.store(smem);
+    vs.store(smem + KRows::BYTES);
+  }
+  __syncthreads();
+
+  const int qlo = (n0 / BMQ) * BMQ;
+  const int qhi = min(T_, p.qend[(int64_t)b * T_ + min(n0 + BNK, T_) - 1]);
+  const int ntile = max(0, (qhi - qlo + BMQ - 1) / BMQ);
+  const int nsb = 2 * ntile;
+
+  // whether (this pair's keys, query sub-block k) has a visible pair, and whether all its pairs are visible: the
+  // producer and the consumer evaluate it identically from the staged doc starts
+  auto sub_state = [&](const int k, const char TNPA_LDS*& base, int& m, int& qb, bool& any, bool& full) {
+    const int t = k >> 1;
+    qb = k & 1;
+    base = smem + (t % NBUF) * BUF;
+    m = qlo + t * BMQ;
+    const int q0 = m + 32 * qb;
+    const int TNPA_LDS* dsl = (const int TNPA_LDS*)(base + DSOFF);
+    const int qlast = min(q0 + 31, T_ - 1);
+    const int ds0 = dsl[32 * qb], dsL = dsl[max(0, qlast - m)];
+    any = uniform_bool(q0 < T_ && ka < T_ && ka <= qlast && ka + 31 >= ds0);
+    full = uniform_bool(ka + 31 <= q0 && dsL <= ka && q0 + 31 < T_);
+  };
+  float gsum[4] = {0.f, 0.f, 0.f, 0.f};
+
+  // Both roles run the same barrier sequence: K/V operands (1), staging prologue (2), one per step, epilogue (4).
+  if (prod) {
+    Op kf[NCK], vf[NCV];
+#pragma unroll
+    for (int c = 0; c < NCK; ++c) kf[c] = read_row<T, KRows>(smem, 32 * pr, l32, c, h);
+#pragma unroll
+    for (int c = 0; c < NCV; ++c) vf[c] = read_row<T, VRows>(smem + KRows::BYTES, 32 * pr, l32, c, h);
+    __syncthreads();
+    __syncthreads();
+    T* dsrow = p.dstile == nullptr ? nullptr
+                                   : (T*)p.dstile + (int64_t)bh * ds_tiles_per_head(T_) * 1024 + l32 * 16 + h * 8;
+    auto produce = [&](const int k, const char TNPA_LDS* base, const int m, const int qb, auto full_c) {
+      constexpr bool FULL = decltype(full_c)::value;
+      f32x16 sacc = zero16(), pacc = zero16();
+#pragma unroll
+      for (int c = 0; c < NCK; ++c) sacc = M::mma(read_row<T, QTile>(base, 32 * qb, kappa<T>(l32), c, h), kf[c], sacc);
+#pragma unroll
+      for (int c = 0; c < NCV; ++c)
+        pacc = M::mma(read_row<T, OTile>(base + QTile::BYTES, 32 * qb, kappa<T>(l32), c, h), vf[c], pacc);
+      // row scale of accumulator row r: query 32 qb + key_off(r, h), two runs of 8 consecutive queries
+      const float TNPA_LDS* rsl = (const float TNPA_LDS*)(base + DSOFF + BMQ * 4) + 32 * qb + 8 * h;
+      float rsr[16];
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        const f32x4 x = *(const f32x4 TNPA_LDS*)(rsl + 16 * (g >> 1) + 4 * (g & 1));
+#pragma unroll
+        for (int i = 0; i < 4; ++i) rsr[4 * g + i] = x[i];
+      }
+      float pv[16], d1[16], d2[16];
+      if constexpr (FULL) {
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          pv[r] = poly_value<POLY, false, PRE>(sacc[r], sacc[r], p.kind, p.deg, p.sm, cf) * rsr[r];
+          poly_grad<POLY, PAR, false, PRE>(sacc[r], sacc[r], pacc[r] * rsr[r], p.kind, p.deg, p.sm, cf, d1[r], d2[r],
+                                           gsum);
+        }
+      } else {
+        const int TNPA_LDS* dsl = (const int TNPA_LDS*)(base + DSOFF);
+        const int key = ka + l32;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int qo = 32 * qb + key_off<T>(r, h);
+          const bool vis = key <= m + qo && dsl[qo] <= key;
+          pv[r] = vis ? poly_value<POLY, false, PRE>(sacc[r], sacc[r], p.kind, p.deg, p.sm, cf) * rsr[r] : 0.f;
+          poly_grad<POLY, PAR, false, PRE>(sacc[r], sacc[r], vis ? pacc[r] * rsr[r] : 0.f, p.kind, p.deg, p.sm, cf,
+                                           d1[r], d2[r], gsum);
+        }
+      }
+      char TNPA_LDS* xs = smem + XOFF + (pr * 2 + (k & 1)) * XSLOT;
+#pragma unroll
+      for (int c2 = 0; c2 < NC2; ++c2) {
+        const Op po = M::cvt(pv + c2 * EPL), so = M::cvt(d1 + c2 * EPL);
+        *(Op TNPA_LDS*)(xs + (c2 * 64 + lane) * 16) = po;
+        *(Op TNPA_LDS*)(xs + ((NC2 + c2) * 64 + lane) * 16) = so;
+        if (dsrow != nullptr) {
+          const int qi = (m >> 5) + qb;
+          __builtin_nontemporal_store(so, (Op*)(dsrow + ((int64_t)qi * (qi + 1) / 2 + (ka >> 5)) * 1024 + 512 * c2));
+        }
+      }
+    };
+    for (int k = 0; k <= nsb; ++k) {
+      if (k < nsb) {
+        const char TNPA_LDS* base;
+        int m, qb;
+        bool any, full;
+        sub_state(k, base, m, qb, any, full);
+        if (full) produce(k, base, m, qb, std::true_type{});
+        else if (any) produce(k, base, m, qb, std::false_type{});
+      }
+      __syncthreads();
+    }
+    // epilogue: the consumers gather dV, then dK, every thread copies the rows out
+    __syncthreads();
+    {
+      Stage<T, BNK, DV, DV, 512> os;
+      os.copy_out(smem, head_ptr_w<T>(p.dv, b, hd), p.dv.st, n0, T_ - n0);
+    }
+    __syncthreads();
+    __syncthreads();
+    {
+      Stage<T, BNK, DK, DK, 512> os;
+      os.copy_out(smem, head_ptr_w<T>(p.dk1, b, hd), p.dk1.st, n0, T_ - n0);
+    }
+  } else {
+    __syncthreads();  // the producers have their K / V operands: the row area is free
+    // staging of the Q (part 0, with the doc starts and row scales) and dO (part 1) rows of a 64-query tile: 4 chunks
+    // of 16 bytes per consumer thread and part, consecutive threads along a row
+    const int ct = (int)threadIdx.x - NPR * 64;
+    u32x4 sr[4];
+    uint32_t qoff[4], ooff[4], loff[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int idx = ct + 256 * i, row = idx >> 4, c = idx & 15;
+      qoff[i] = (uint32_t)(((int64_t)row * p.q1.st + c * 8) * 2);
+      ooff[i] = (uint32_t)(((int64_t)row * dost + c * 8) * 2);
+      loff[i] = QTile::off(row, c * 8);
+    }
+    int dsv = 0;
+    float scv = 0.f;
+    auto load_part = [&](const int part, const int m) {
+      if (part == 0) {
+        const auto rs = rows_rsrc<T>(qp, p.q1.st, m, T_, DK);
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+          sr[i] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rs, (int)qoff[i], 0, 0));
+        if (ct < BMQ) {
+          const int q = m + ct;
+          dsv = q < T_ ? dst[q] : INT_MAX;
+          scv = p.dpre ? 1.0f : (q < T_ ? rsc[q] : 0.f);
+        }
+      } else {
+        const auto rs = rows_rsrc<T>(dop, dost, m, T_, DV);
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+          sr[i] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rs, (int)ooff[i], 0, 0));
+      }
+    };
+    auto store_part = [&](const int part, char TNPA_LDS* buf) {
+      char TNPA_LDS* tb = buf + (part ? QTile::BYTES : 0);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) *(u32x4 TNPA_LDS*)(tb + loff[i]) = sr[i];
+      if (part == 0 && ct < BMQ) {
+        ((int TNPA_LDS*)(buf + DSOFF))[ct] = dsv;
+        ((float TNPA_LDS*)(buf + DSOFF + BMQ * 4))[ct] = scv;
+      }
+    };
+    // tiles 0 and 1 in LDS before the loop (the dO part of tile 1 is written in step 0); tile u >= 2 is loaded in
+    // steps 2u-4 (Q) and 2u-3 (dO) and written one step later, into the buffer of tile u-3 (last read in step 2u-4)
+    load_part(0, qlo);
+    store_part(0, smem);
+    load_part(1, qlo);
+    store_part(1, smem);
+    load_part(0, qlo + BMQ);
+    store_part(0, smem + BUF);
+    load_part(1, qlo + BMQ);
+    __syncthreads();
+
+    f32x16 dv[NDV], dk[NDK];
+#pragma unroll
+    for (int d = 0; d < NDV; ++d) dv[d] = zero16();
+#pragma unroll
+    for (int d = 0; d < NDK; ++d) dk[d] = zero16();
+    auto consume = [&](const int k) {
+      const char TNPA_LDS* base;
+      int m, qb;
+      bool any, full;
+      sub_state(k, base, m, qb, any, full);
+      if (!any) return;
+      const char TNPA_LDS* xs = smem + XOFF + (pr * 2 + (k & 1)) * XSLOT;
+      Op po[NC2], so[NC2];
+#pragma unroll
+      for (int c2 = 0; c2 < NC2; ++c2) {
+        po[c2] = *(const Op TNPA_LDS*)(xs + (c2 * 64 + lane) * 16);
+        so[c2] = *(const Op TNPA_LDS*)(xs + ((NC2 + c2) * 64 + lane) * 16);
+      }
+#pragma unroll
+      for (int d = 0; d < NDV; ++d)
+#pragma unroll
+        for (int c2 = 0; c2 < NC2; ++c2)
+          dv[d] = M::mma(read_col<T, OTile>(base + QTile::BYTES, 32 * qb + c2 * KC, 32 * d, lane), po[c2], dv[d]);
+#pragma unroll
+      for (int d = 0; d < NDK; ++d)
+#pragma unroll
+        for (int c2 = 0; c2 < NC2; ++c2)
+          dk[d] = M::mma(read_col<T, QTile>(base, 32 * qb + c2 * KC, 32 * d, lane), so[c2], dk[d]);
+    };
+    for (int k = 0; k <= nsb; ++k) {
+      const int kp = k - 1;
+      store_part(kp & 1, smem + (((kp >> 1) + 2) % NBUF) * BUF);
+      load_part(k & 1, qlo + ((k >> 1) + 2) * BMQ);
+      if (k >= 1) consume(k - 1);
+      __syncthreads();
+    }
+    // epilogue: dV rows, then dK rows, through LDS; every thread copies them out
+    acc_rows_to_lds<T, VRows, NDV>(smem, 32 * pr, l32, h, dv, p.vf, DV);
+    __syncthreads();
+    {
+      Stage<T, BNK, DV, DV, 512> os;
+      os.copy_out(smem, head_ptr_w<T>(p.dv, b, hd), p.dv.st, n0, T_ - n0);
+    }
+    __syncthreads();
+    acc_rows_to_lds<T, KRows, NDK>(smem, 32 * pr, l32, h, dk, p.gf, DK);
+    __syncthreads();
+    {
+      Stage<T, BNK, DK, DK, 512> os;
+      os.copy_out(smem, head_ptr_w<T>(p.dk1, b, hd), p.dk1.st, n0, T_ - n0);
+    }
+  }
+
+  if constexpr (PAR) {
+    if (p.dpar != nullptr) {
+      // fixed-order reduction: lanes (butterfly), then the producer waves in index order
+      if (prod) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          float x = gsum[i];
+#pragma unroll
+          for (int o = 32; o >= 1; o >>= 1) x += __shfl_xor(x, o, 64);
+          if (lane == 0) red_[pr][i] = x;
+        }
+      }
+      __syncthreads();
+      if (threadIdx.x < 4) {
+        float acc = 0.f;
+        for (int w = 0; w < NPR; ++w) acc += red_[w][threadIdx.x];
+        p.dpar[((int64_t)bh * NNB + nb) * 4 + threadIdx.x] = acc;
+      }
+    }
+  }
+}
+
+// ------------------------------------------------------------------------------------------------ dQ from dS
+// dQ = gf * dS K from the dS tiles the dK pass stored: one matrix product per (query, key) sub-block instead of the
+// S and dP recompute of k_bwd_q. A workgroup owns BM = NW*32 queries; wave w accumulates dQ^T = K^T dS^T for its
+// 32-query subtile (lane <-> query). K tiles of BN keys go through three LDS buffers shared by the workgroup (one
+// barrier per tile); each wave's dS tiles come from global memory straight into registers two tiles ahead, then
+// through a private LDS area of the wave, whose transposed read yields the lane <-> query operand (no barrier: a
+// wave reads back only what it wrote). A sub-block without a visible (query, key) pair is skipped and its tile never
+// read (its load is pointed past the buffer resource, which returns zeros without a memory access); the dK pass
+// stores every sub-block that has one. Same operand rounding as ref: tnlm/kernels/poly_attn.py:196-200 (dS cast to
+// the input dtype before the K product, FP32 accumulation).
+#ifndef TNPA_DS_LOAD_AUX
+#define TNPA_DS_LOAD_AUX 2
+#endif
+template <typename T, int DK, int NW, int BN>
+__global__ void __attribute__((amdgpu_flat_work_group_size(NW * 64, NW * 64), amdgpu_waves_per_eu(2)))
+k_bwd_q_ds(const KParams p) {
+  typedef Mfma<T> M;
+  typedef typename M::Op Op;
+  constexpr int KC = M::KC, NT = NW * 64, NDK = DK / 32, NKB = BN / 32, NC2 = 32 / KC;
+  constexpr int BM = NW * 32;
+  typedef Tile<T, BN, DK> KTile;
+  typedef Tile<T, 32, 32> STile;  // one dS sub-block: rows = keys, columns = queries
+  typedef Tile<T, BM, DK> QTile;
+  typedef Stage<T, BN, DK, DK, NT> KStage;
+  static_assert(sizeof(T) == 2 && KStage::TOTAL % NT == 0, "16-bit types, K tiles split evenly over the threads");
+  constexpr int NBUF = 3;
+  constexpr int PRIV = 2 * NKB * STile::BYTES;  // per wave: the dS tiles of two steps
+  constexpr int KOFF = NW * PRIV;
+  constexpr int SMEM = cmax(KOFF + NBUF * KTile::BYTES, QTile::BYTES);
+  static_assert(SMEM <= 160 * 1024, "LDS");
+  __shared__ __attribute__((aligned(16))) char smem_[SMEM];
+  char TNPA_LDS* smem = (char TNPA_LDS*)smem_;
+
+  const int T_ = p.T, BH = p.B * p.H;
+  const int NMB = (T_ + BM - 1) / BM;
+  const int item = blockIdx.x;
+  const int mb = NMB - 1 - item / BH, bh = item % BH, b = bh / p.H, hd = bh % p.H;
+  const int m0 = mb * BM;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, h = lane >> 5, l32 = lane & 31;
+  const T* kp = head_ptr<T>(p.k1, b, hd);
+  const int* dst = p.dstart + (int64_t)b * T_;
+  const int qa = m0 + wave * 32, q = qa + l32;
+  const int dsq = q < T_ ? dst[q] : INT_MAX;  // first key visible from query q (q + 1 for padding)
+  const int qi = qa >> 5;
+  // buffer resource over the wave's row of dS tiles (tiles j = 0 .. qi of query sub-block qi)
+  const T* trow = (const T*)p.dstile + ((int64_t)bh * ds_tiles_per_head(T_) + (int64_t)qi * (qi + 1) / 2) * 1024;
+  const int tbytes = qa < T_ ? (qi + 1) * 2048 : 0;
+  const auto srs = __builtin_amdgcn_make_buffer_rsrc((void*)trow, (short)0, tbytes, 0x00020000);
+  const uint32_t soff = (uint32_t)(l32 * 32 + h * 16);  // + 1024 * c2 + 2048 * j
+  char TNPA_LDS* priv = smem + wave * PRIV;
+  char TNPA_LDS* kbuf = smem + KOFF;
+
+  // sub-block (wave's queries, keys key0 .. key0 + 31) has a visible pair: wave-uniform
+  auto visible = [&](const int key0) {
+    const bool v = q < T_ && max(dsq, key0) <= min(q, key0 + 31);
+    return __builtin_amdgcn_readfirstlane((int)(__ballot(v) != 0)) != 0;
+  };
+  u32x4 sreg[2][NKB][NC2];
+  auto load_ds = [&](u32x4 (&r)[NKB][NC2], const int n0) {
+#pragma unroll
+    for (int kb = 0; kb < NKB; ++kb) {
+      const int key0 = n0 + 32 * kb;
+      const uint32_t base = visible(key0) ? (uint32_t)((key0 >> 5) * 2048) : (uint32_t)tbytes;
+#pragma unroll
+      for (int c2 = 0; c2 < NC2; ++c2)
+        r[kb][c2] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(srs, (int)(base + soff + 1024 * c2), 0, TNPA_DS_LOAD_AUX));
+    }
+  };
+  auto store_ds = [&](char TNPA_LDS* pt, const u32x4 (&r)[NKB][NC2]) {
+#pragma unroll
+    for (int kb = 0; kb < NKB; ++kb)
+#pragma unroll
+      for (int c2 = 0; c2 < NC2; ++c2)
+        *(u32x4 TNPA_LDS*)(pt + kb * STile::BYTES + STile::off(l32, 16 * c2 + 8 * h)) = r[kb][c2];
+  };
+
+  const int lo = (dst[m0] / BN) * BN;
+  const int hi = min(m0 + BM, T_);
+  const int ntile = (hi - lo + BN - 1) / BN;
+  KStage ks;
+  uint32_t kvo[KStage::PER];
+#pragma unroll
+  for (int i = 0; i < KStage::PER; ++i) kvo[i] = KStage::chunk_off(i, p.k1.st);
+  auto load_k = [&](const int n1) {
+    const auto rs = rows_rsrc<T>(kp, p.k1.st, n1, T_, DK);
+#pragma unroll
+    for (int i = 0; i < KStage::PER; ++i) ks.load_buf(i, rs, kvo[i]);
+  };
+  auto store_k = [&](char TNPA_LDS* dstb) {
+#pragma unroll
+    for (int i = 0; i < KStage::PER; ++i) ks.store_raw(i, dstb);
+  };
+
+  f32x16 dq[NDK];
+#pragma unroll
+  for (int d = 0; d < NDK; ++d) dq[d] = zero16();
+
+  // prologue: K tile 0 into buffer 0, K tile 1 into registers; dS of tiles 0 and 1 into the two register sets
+  load_k(lo);
+  load_ds(sreg[0], lo);
+  store_k(kbuf);
+  load_k(lo + BN);
+  load_ds(sreg[1], lo + BN);
+  __syncthreads();
+
+  int cur = 0;
+  auto next_buf = [](const int c) { return c + 1 == NBUF ? 0 : c + 1; };
+  auto step = [&](const int j, auto par_c) {
+    constexpr int P = decltype(par_c)::value;
+    const int n0 = lo + j * BN;
+    char TNPA_LDS* pt = priv + P * NKB * STile::BYTES;
+    store_ds(pt, sreg[P]);
+    load_ds(sreg[P], n0 + 2 * BN);
+    const int nb = next_buf(cur);
+    store_k(kbuf + nb * KTile::BYTES);
+    load_k(n0 + 2 * BN);
+    const char TNPA_LDS* kt = kbuf + cur * KTile::BYTES;
+#pragma unroll
+    for (int kb = 0; kb < NKB; ++kb) {
+      if (!visible(n0 + 32 * kb)) continue;
+      Op bs[NC2];
+#pragma unroll
+      for (int c2 = 0; c2 < NC2; ++c2) bs[c2] = read_col<T, STile>(pt + kb * STile::BYTES, c2 * KC, 0, lane);
+#pragma unroll
+      for (int c2 = 0; c2 < NC2; ++c2)
+#pragma unroll
+        for (int d = 0; d < NDK; ++d) {
+          const Op a = read_col<T, KTile>(kt, 32 * kb + c2 * KC, 32 * d, lane);
+          dq[d] = M::mma(a, bs[c2], dq[d]);
+        }
+    }
+    __syncthreads();
+    cur = nb;
+  };
+  for (int j = 0; j < ntile; j += 2) {
+    step(j, std::integral_constant<int, 0>{});
+    if (j + 1 < ntile) step(j + 1, std::integral_constant<int, 1>{});
+  }
+
+  // dQ rows: scaled by the chain-rule factor, gathered in LDS, written as whole rows
+  __syncthreads();
+  acc_rows_to_lds<T, QTile, NDK>(smem, 32 * wave, l32, h, dq, p.gf, DK);
+  __syncthreads();
+  Stage<T, BM, DK, DK, NT> os;
+  os.copy_out(smem, head_ptr_w<T>(p.dq1, b, hd), p.dq1.st, m0, T_ - m0);
+}
+
 // ------------------------------------------------------------------------------------------------ launchers
 template <typename T, int POLY, int DK, int DV> hipError_t launch_fwd(const KParams& p, hipStream_t st) {
   typedef Cfg<T, POLY, DK, DV> C;
@@ -1356,6 +1821,11 @@ template <typename T, int POLY, int DK, int DV> hipError_t launch_fwd(const KPar
 template <typename T, int POLY, int DK, int DV> hipError_t launch_bwd_kv(const KParams& p, hipStream_t st) {
   typedef Cfg<T, POLY, DK, DV> C;
   static_assert(C::KV_KEYS == (C::KV_SPLIT ? 256 : 128), "dK/dV block size mirrors kv_block_keys()");
+  if constexpr (kv_pair_cfg<T, POLY, DK, DV>()) {
+    const int grid = p.B * p.H * ((p.T + 127) / 128);
+    hipLaunchKernelGGL((k_bwd_kv_pair<T, POLY, DK, DV>), dim3(grid), dim3(512), 0, st, p);
+    return hipGetLastError();
+  }
   const int grid = p.B * p.H * ((p.T + C::KV_KEYS - 1) / C::KV_KEYS);
   if constexpr (C::KV_SPLIT) {
     if (p.kvsel & 1)
@@ -1378,6 +1848,17 @@ template <typename T, int POLY, int DK, int DV> hipError_t launch_bwd_q(const KP
   hipLaunchKernelGGL((k_bwd_q<T, POLY, DK, DV, C::BQ_NW, C::BQ_QW, C::BQ_BN, C::BQ_WPE>), dim3(grid), dim3(C::BQ_NW * 64), 0, st,
                      p);
   return hipGetLastError();
+}
+
+template <typename T, int DK> hipError_t launch_bwd_q_ds(const KParams& p, hipStream_t st) {
+  if constexpr (sizeof(T) == 2 && DK == 128) {
+    constexpr int NW = 8, BN = 64, BM = NW * 32;
+    const int grid = p.B * p.H * ((p.T + BM - 1) / BM);
+    hipLaunchKernelGGL((k_bwd_q_ds<T, DK, NW, BN>), dim3(grid), dim3(NW * 64), 0, st, p);
+    return hipGetLastError();
+  } else {
+    return hipErrorInvalidValue;
+  }
 }
 
 }  // namespace tnpa

@@ -31,6 +31,7 @@ struct KParams {
   const float* offs;   // (H) offset_square offsets or null
   float* norms;        // (NPAIR, 2, H) max row norms of q and k (forward), or null
   float* dpar;         // (B*H, NNB, 4) per-key-block partial sums for dcoef / db, or null
+  void* dstile;        // dS tiles written by the dK pass and read by the dQ-from-dS kernel, or null (see ds_tile_*)
   int dpre;            // 1: dsc holds the row-scaled dout; 0: the dK/dV pass scales dout while staging it
   int kvsel;           // key-side kernels to launch: 1 = dV pass, 2 = dK pass, 3 = both (or the combined kernel)
   int B, H, T;
@@ -46,9 +47,20 @@ inline bool kv_split(bool f32, int poly, int dk, int dv) {
   return !f32 && !two_pair_poly(poly) && (dk > 64 || dv > 64);
 }
 
+// Whether the key side is the wave-pair kernel k_bwd_kv_pair (16-bit inputs, one q/k pair, head dims 128): one launch
+// computing S and dP once per sub-block, in place of the separate dV and dK passes.
+constexpr bool kv_pair(bool f32, int poly, int dk, int dv) {
+  return !f32 && !two_pair_poly(poly) && dk == 128 && dv == 128;
+}
+template <typename T, int POLY, int DK, int DV> constexpr bool kv_pair_cfg() {
+  return kv_pair(sizeof(T) == 4, POLY, DK, DV);
+}
+
 // Keys per dK/dV workgroup (sizes the dcoef/db partials); mirrors Cfg::KV_KEYS: eight waves of 32 keys for the split
-// passes, four waves for the combined kernel.
-inline int kv_block_keys(bool f32, int poly, int dk, int dv) { return kv_split(f32, poly, dk, dv) ? 256 : 128; }
+// passes, four waves (or four wave pairs) for the combined kernels.
+inline int kv_block_keys(bool f32, int poly, int dk, int dv) {
+  return kv_split(f32, poly, dk, dv) && !kv_pair(f32, poly, dk, dv) ? 256 : 128;
+}
 
 // Whether the dK/dV passes scale dO by the row scale themselves at no cost: they stage the dO rows a step ahead and
 // apply the factor when writing them to LDS (three-buffer staging; 16-bit inputs, one q/k pair, and 64-row tiles
@@ -59,8 +71,23 @@ constexpr bool kv_scales_in_pass(bool f32, int poly, int dk, int dv) {
   return !f32 && !two_pair_poly(poly) && (8 * dk) % nt == 0 && (8 * dv) % nt == 0;
 }
 
+// dS tiles: the masked, row-scaled gradient dS of every 32x32 (query, key) sub-block i >= j of one (b, h) head,
+// rounded to the input dtype, 1024 elements each, lower-triangular order (tile i*(i+1)/2 + j), heads one after
+// another. Inside a tile, element (key kk, query qq) sits at 512*(qq/16) + 16*kk + qq%16: the dK pass's register
+// layout (lane kk + 32*((qq/8)%2) holds queries 8*((qq/8)%2) + 16*c .. +7 of chunk c = qq/16), so each of its two
+// 16-byte stores per lane writes one contiguous KiB.
+__host__ __device__ inline int ds_tile_rows(int T) { return (T + 31) / 32; }
+__host__ __device__ inline int64_t ds_tiles_per_head(int T) {
+  const int64_t n = ds_tile_rows(T);
+  return n * (n + 1) / 2;
+}
+inline int64_t ds_tile_bytes(int B, int H, int T, int esize) {
+  return (int64_t)B * H * ds_tiles_per_head(T) * 1024 * esize;
+}
+
 template <typename T, int POLY, int DK, int DV> hipError_t launch_fwd(const KParams& p, hipStream_t st);
 template <typename T, int POLY, int DK, int DV> hipError_t launch_bwd_kv(const KParams& p, hipStream_t st);
 template <typename T, int POLY, int DK, int DV> hipError_t launch_bwd_q(const KParams& p, hipStream_t st);
+template <typename T, int DK> hipError_t launch_bwd_q_ds(const KParams& p, hipStream_t st);
 
 }  // namespace tnpa

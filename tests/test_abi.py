@@ -148,15 +148,20 @@ def test_misaligned_views_and_missing_parameters_are_rejected(lib):
 
 
 def test_backward_workspace_size(lib):
-    """The workspace holds the fixed-order dcoef/db partials (one float4 per (b, h, key block)) and, where the plan
-    streams it, row_scale * dO in the problem dtype; each part rounded up to 256 bytes."""
+    """The workspace holds the fixed-order dcoef/db partials (one float4 per (b, h, key block)), where the plan
+    streams it row_scale * dO in the problem dtype, and where dQ is computed from stored dS the dS tiles (one
+    32x32 tile of the input dtype per sub-block on or below the diagonal); each part rounded up to 256 bytes."""
     from tensor_train_ing_amd import _abi
     r = lambda n: -(-n // 256) * 256  # noqa: E731
     assert lib.tnpa_backward_workspace_bytes(ctypes.byref(_problem())) == 0
     p = _problem(kind=_abi.OFFSET_SQUARE, offset=4096, seq_len=300)  # bf16, head dim 64: four-wave 128-key blocks
     assert lib.tnpa_backward_workspace_bytes(ctypes.byref(p)) == r(2 * 2 * 3 * 4 * 4)
-    p = _problem(kind=_abi.OFFSET_SQUARE, offset=4096, seq_len=300, head_dim_k=128, head_dim_v=128)  # 256-key blocks
-    assert lib.tnpa_backward_workspace_bytes(ctypes.byref(p)) == r(2 * 2 * 2 * 4 * 4)
+    p = _problem(kind=_abi.OFFSET_SQUARE, offset=4096, seq_len=300, head_dim_k=128, head_dim_v=128)  # 128-key pairs
+    tiles = 10 * 11 // 2  # 32-row sub-blocks of T=300: 10, tiles on or below the diagonal: 55
+    assert lib.tnpa_backward_workspace_bytes(ctypes.byref(p)) == r(2 * 2 * 3 * 4 * 4) + r(2 * 2 * tiles * 1024 * 2)
+    assert lib.tnpa_x_workspace_bytes(ctypes.byref(p), _abi.X_DS_OFF) == r(2 * 2 * 3 * 4 * 4)
+    p = _problem(kind=_abi.OFFSET_SQUARE, offset=4096, seq_len=300, head_dim_k=128, head_dim_v=64)  # 256-key passes
+    assert lib.tnpa_x_workspace_bytes(ctypes.byref(p), _abi.X_DS_OFF) == r(2 * 2 * 2 * 4 * 4)
     # lower_degree_mix (two pairs) streams the row-scaled dO: partials, then (B, H, T, dv) bf16
     p = _problem(kind=_abi.LOWER_DEGREE_MIX, coef=4096, seq_len=300)
     assert lib.tnpa_backward_workspace_bytes(ctypes.byref(p)) == r(2 * 2 * 3 * 4 * 4) + r(2 * 2 * 300 * 64 * 2)
@@ -176,15 +181,20 @@ def _launches(lib, p, opts=0):
 def test_backward_plan(lib):
     """Which launches tnpa_backward makes: the row-scaled dO only where the key side cannot scale dO for free (fp32,
     two q/k pairs, or a head dim too small for the three-buffer tile split); separate dV and dK passes for 16-bit one
-    q/k pair at a head dim above 64; the dpar reduction for the kinds with head parameters."""
+    q/k pair at a head dim above 64, except head dims 128 / 128, whose key side is the one wave-pair kernel; dQ from
+    the dS tiles at key head dim 128 (dQ recomputing S and dP otherwise, or with X_DS_OFF); the dpar reduction for
+    the kinds with head parameters."""
     from tensor_train_ing_amd import _abi
     assert _launches(lib, _problem()) == ["kv", "q"]
-    assert _launches(lib, _problem(head_dim_k=128, head_dim_v=128)) == ["dv", "dk", "q"]
-    assert _launches(lib, _problem(dtype=_abi.F16, head_dim_k=128, head_dim_v=128)) == ["dv", "dk", "q"]
+    assert _launches(lib, _problem(head_dim_k=128, head_dim_v=128)) == ["kv", "qds"]
+    assert _launches(lib, _problem(dtype=_abi.F16, head_dim_k=128, head_dim_v=128)) == ["kv", "qds"]
+    assert _launches(lib, _problem(head_dim_k=128, head_dim_v=128), _abi.X_DS_OFF) == ["kv", "q"]
+    assert _launches(lib, _problem(head_dim_k=64, head_dim_v=128)) == ["dv", "dk", "q"]
+    assert _launches(lib, _problem(dtype=_abi.F32, head_dim_k=128, head_dim_v=128)) == ["scale", "kv", "q"]
     assert _launches(lib, _problem(dtype=_abi.F32)) == ["scale", "kv", "q"]
     assert _launches(lib, _problem(kind=_abi.SIGNED_PRODUCT)) == ["scale", "kv", "q"]
     assert _launches(lib, _problem(head_dim_v=16)) == ["scale", "kv", "q"]
-    assert _launches(lib, _problem(head_dim_k=128, head_dim_v=32)) == ["scale", "dv", "dk", "q"]
+    assert _launches(lib, _problem(head_dim_k=128, head_dim_v=32)) == ["scale", "dv", "dk", "qds"]
     assert _launches(lib, _problem(head_dim_v=32)) == ["kv", "q"]
     assert _launches(lib, _problem(kind=_abi.OFFSET_SQUARE, offset=4096)) == ["kv", "q", "dpar"]
     assert _launches(lib, _problem(kind=_abi.LOWER_DEGREE_MIX, coef=4096)) == ["scale", "kv", "q", "dpar"]

@@ -1,6 +1,9 @@
 """tnpa_backward_noalloc (the allocation-free backward, with its scratch in a fixed device array) against
-tnpa_backward (caller-allocated workspace), called through the C ABI: bit-identical gradients and dcoef/db on two
-calls in a row, the second on a smaller problem, so stale scratch from the first call cannot leak into the second."""
+tnpa_backward (caller-allocated workspace), called through the C ABI, on two calls in a row, the second on a smaller
+problem, so stale scratch from the first call cannot leak into the second: bit-identical dK, dV and dcoef/db, and
+bit-identical dQ except where tnpa_backward computes dQ from stored dS tiles (16-bit, one q/k pair, head dim 128),
+which its fixed scratch cannot hold: there both dQ agree to 5e-3 relative Frobenius (S rounded inside a different
+pair of products), within the bf16 tolerance of the reference."""
 from __future__ import annotations
 
 import ctypes
@@ -8,7 +11,7 @@ import ctypes
 import pytest
 import torch
 
-from poly_ref import gaussian_inputs, row_scale
+from poly_ref import gaussian_inputs, rel_fro, row_scale
 
 pytestmark = pytest.mark.gpu
 
@@ -53,7 +56,10 @@ def test_noalloc_backward_equals_workspace_backward(kind, D):
         b = _run("tnpa_backward_noalloc", kind, B, H, T, D, seed)
         for n in a:
             assert torch.isfinite(a[n]).all(), n
-            assert torch.equal(a[n], b[n]), (kind, D, T, n)
+            if n == "dq1" and D == 128 and kind in ("power", "offset_square"):
+                assert rel_fro(a[n], b[n]) < 5e-3, (kind, D, T, n)
+            else:
+                assert torch.equal(a[n], b[n]), (kind, D, T, n)
 
 
 def test_noalloc_rejects_problems_beyond_its_scratch():
