@@ -153,15 +153,22 @@ def kernel_times(kind, q, k, q2, k2, v, do, doc, rs, degree, reps):
     return out
 
 
-def measured_traffic(config, kernel):
-    """HBM bytes per launch of `kernel` from the committed rocprofv3 FETCH_SIZE / WRITE_SIZE summary
-    (profiles/hbm_traffic_<config>.txt, counters scaled by a plain-copy calibration), or None if not profiled."""
+# kernel symbol names (as the rocprofv3 summaries list them) of each backward-plan launch
+LAUNCH_KERNELS = {"fwd": ("k_fwd",), "kv": ("k_bwd_kv_pair", "k_bwd_kv"), "dv": ("k_bwd_kv",), "dk": ("k_bwd_kv",),
+                  "q": ("k_bwd_q",), "qds": ("k_bwd_q_ds",)}
+
+
+def measured_traffic(config, launch):
+    """HBM bytes per dispatch of the kernel behind backward-plan launch `launch` from the committed rocprofv3
+    FETCH_SIZE / WRITE_SIZE summary (profiles/hbm_traffic_<config>.txt, counters scaled by a plain-copy
+    calibration), or None if not profiled."""
     path = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles", f"hbm_traffic_{config}.txt")
+    names = LAUNCH_KERNELS.get(launch, (launch,))
     try:
         with open(path) as f:
             for line in f:
                 parts = line.split()
-                if len(parts) == 4 and parts[0] == kernel:
+                if len(parts) == 4 and parts[0] in names:
                     return int(parts[3])
     except OSError:
         pass
