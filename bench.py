@@ -48,7 +48,7 @@ CONFIGS = {  # name: (B, H, T, D, degree, boost_rows, seed) -- BASELINE.json con
 # pairs one more S, dK and dQ each. The dO row-scaling pass and the dpar reduction are bandwidth kernels with no
 # matrix work.
 UNITS_ONE = {"fwd": 2, "dv": 2, "dk": 3, "kv": 4, "q": 3, "qds": 1, "scale": 0, "dpar": 0}
-UNITS_TWO = {"fwd": 3, "kv": 6, "q": 5, "scale": 0, "dpar": 0}
+UNITS_TWO = {"fwd": 3, "kv": 6, "q": 5, "qds": 2, "scale": 0, "dpar": 0}
 
 
 def npairs(T, doc_len=0):

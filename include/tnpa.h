@@ -74,10 +74,10 @@ typedef struct {
  * kinds and ignored otherwise. workspace is caller-allocated device memory of at least
  * tnpa_backward_workspace_bytes(problem) bytes, 256-byte aligned (NULL when that is 0); its contents on entry do not
  * matter and on return are unspecified. It stands for the reference's per-call scratch (the DPAR partials of
- * ref: tnlm/kernels/poly_attn.py:296), so the library itself never allocates. For 16-bit inputs with one q/k pair at
- * head dim 128 it also holds the bf16/fp16 gradient dS of every 32x32 (query, key) sub-block on or below the
- * diagonal (about B*H*T^2 bytes, 545 MB at B8 H16 T2048; only while that stays within 4 GiB), from which dQ is
- * computed with one matrix product instead of recomputing S and dP. */
+ * ref: tnlm/kernels/poly_attn.py:296), so the library itself never allocates. For 16-bit inputs at key head dim
+ * 128 it also holds the bf16/fp16 gradient dS of every 32x32 (query, key) sub-block on or below the diagonal, one
+ * set per q/k pair (about B*H*T^2 bytes per pair, 545 MB at B8 H16 T2048; only while all sets stay within 4 GiB),
+ * from which each dQ is computed with one matrix product instead of recomputing S (both pairs) and dP. */
 typedef struct {
   tnpa_tensor_t dout, dq1, dk1, dq2, dk2, dv;
   float* dpar;
@@ -116,7 +116,7 @@ int tnpa_backward(const tnpa_problem_t* problem, const tnpa_grads_t* grads, void
  * (code under HIP graph capture, tight serving loops, harnesses that forbid hipMalloc). No counterpart in the
  * reference. The same results as tnpa_backward (it runs the plan that streams no row-scaled dO, bit-identical to
  * tnpa_backward's, except that dQ is recomputed from S and dP where tnpa_backward reads the dS tiles it stored in its
- * workspace: 16-bit, one q/k pair, head dim 128; the two dQ then differ only by rounding inside the products);
+ * workspace: 16-bit, key head dim 128; the two dQ then differ only by rounding inside the products);
  * grads->workspace and workspace_bytes are ignored. Its scratch is a fixed 1 MiB array in each
  * GPU's memory (the dcoef/db partials: B * H * ceil(T / 128 or 256) * 16 bytes), held until the process ends;
  * problems that need more fail with TNPA_ERR_UNSUPPORTED before anything is enqueued. Every call on one GPU shares

@@ -377,7 +377,7 @@ struct Plan {
   int what[6] = {0, 0, 0, 0, 0, 0};
   bool prescale = false, par = false, ds = false;
   int nnb = 0;  // key blocks per row (dpar partials)
-  int64_t dpar_off = 0, dos_off = 0, ds_off = 0, bytes = 0;
+  int64_t dpar_off = 0, dos_off = 0, ds_off = 0, ds2_off = 0, bytes = 0;
 };
 
 int64_t align256(int64_t x) { return (x + 255) & ~(int64_t)255; }
@@ -398,11 +398,16 @@ int make_plan(const tnpa_problem_t& p, int opts, Plan& pl) {
   const int64_t dpar_bytes = pl.par ? (int64_t)p.batch * p.heads * pl.nnb * 4 * (int64_t)sizeof(float) : 0;
   const int64_t dos_bytes = pl.prescale ? (int64_t)p.batch * p.heads * p.seq_len * dv * esize(p.dtype) : 0;
   const int64_t ds_bytes = tnpa::ds_tile_bytes(p.batch, p.heads, p.seq_len, esize(p.dtype));
-  pl.ds = split && !f32 && dk == 128 && !(opts & TNPA_X_DS_OFF) && ds_bytes <= kMaxDsTileBytes;
+  // dS tiles (one set per q/k pair) where the key side forms dS in a dK pass (one pair) or in the combined kernel
+  // (two pairs), for 16-bit inputs at key head dim 128
+  const int npairs = tnpa::two_pair_poly(poly) ? 2 : 1;
+  pl.ds = (split || npairs == 2) && !f32 && dk == 128 && !(opts & TNPA_X_DS_OFF) &&
+          npairs * ds_bytes <= kMaxDsTileBytes;
   pl.dpar_off = 0;
   pl.dos_off = align256(dpar_bytes);
   pl.ds_off = pl.dos_off + align256(dos_bytes);
-  pl.bytes = pl.ds_off + (pl.ds ? align256(ds_bytes) : 0);
+  pl.ds2_off = pl.ds_off + align256(ds_bytes);
+  pl.bytes = pl.ds_off + (pl.ds ? npairs * align256(ds_bytes) : 0);
   if (pl.prescale) pl.what[pl.n++] = L_SCALE;
   if (split && !tnpa::kv_pair(f32, poly, dk, dv)) {
     pl.what[pl.n++] = L_DV;
@@ -454,7 +459,10 @@ int run_backward(const tnpa_problem_t* problem, const tnpa_grads_t* grads, int o
     k.dsc = desc(dos);
     k.dpre = 1;
   }
-  if (pl.ds) k.dstile = ws + pl.ds_off;
+  if (pl.ds) {
+    k.dstile = ws + pl.ds_off;
+    if (two_pairs(p.kind)) k.dstile2 = ws + pl.ds2_off;
+  }
   for (int i = 0; i < pl.n; ++i) {
     if (only != -1 && i != only) continue;
     hipError_t e = hipSuccess;
@@ -470,10 +478,17 @@ int run_backward(const tnpa_problem_t* problem, const tnpa_grads_t* grads, int o
       case L_DV: k.kvsel = 1; e = run(PH_BWD_KV, p, k, stream); break;
       case L_DK: k.kvsel = 2; e = run(PH_BWD_KV, p, k, stream); break;
       case L_Q: e = run(PH_BWD_Q, p, k, stream); break;
-      case L_QDS:
-        e = p.dtype == TNPA_BF16 ? tnpa::launch_bwd_q_ds<__bf16, 128>(k, stream)
-                                 : tnpa::launch_bwd_q_ds<_Float16, 128>(k, stream);
+      case L_QDS: {
+        // dQ1 = dS1 K1, then (two pairs) dQ2 = dS2 K2 with the same kernel
+        tnpa::KParams k2 = k;
+        k2.k1 = k.k2;
+        k2.dq1 = k.dq2;
+        k2.dstile = k.dstile2;
+        for (int pr = 0; pr < (two_pairs(p.kind) ? 2 : 1) && e == hipSuccess; ++pr)
+          e = p.dtype == TNPA_BF16 ? tnpa::launch_bwd_q_ds<__bf16, 128>(pr ? k2 : k, stream)
+                                   : tnpa::launch_bwd_q_ds<_Float16, 128>(pr ? k2 : k, stream);
         break;
+      }
       case L_DPAR: {
         const int n = p.heads * 4;
         hipLaunchKernelGGL(k_dpar_reduce, dim3((n + 255) / 256), dim3(256), 0, stream, (const float*)k.dpar, p.batch,

@@ -1155,21 +1155,30 @@ k_bwd_kv(const KParams p) {
         }
       }
     }
-    // the dK pass of a one-pair 16-bit kind also stores dS for the dQ-from-dS kernel: tile (query sub-block,
-    // key sub-block), each of its two operands one contiguous KiB (layout at ds_tile_rows)
-    if constexpr (MODE == KV_DK && NPAIR == 1 && sizeof(T) == 2) {
-      if (p.dstile != nullptr) {
-        const int qi = (m >> 5) + qb;
-        T* tb = (T*)p.dstile + ((int64_t)bh * ds_tiles_per_head(T_) + (int64_t)qi * (qi + 1) / 2) * 1024 + l32 * 16 + h * 8;
+    // the dK pass of a one-pair 16-bit kind, and the combined kernel of a two-pair one, also store dS (dS1 and dS2)
+    // for the dQ-from-dS kernel: tile (query sub-block, key sub-block), each of its two operands one contiguous KiB
+    // (layout at ds_tile_rows). Issued between the dV and dK products for lower_degree_mix, after the dK products
+    // otherwise (same-process timing of the three positions).
+    auto store_ds = [&]() {
+      if constexpr (((MODE == KV_DK && NPAIR == 1) || (MODE == KV_BOTH && NPAIR == 2)) && sizeof(T) == 2) {
+        if (p.dstile != nullptr) {
+          const int qi = (m >> 5) + qb;
+          const int64_t toff = ((int64_t)bh * ds_tiles_per_head(T_) + (int64_t)qi * (qi + 1) / 2) * 1024 + l32 * 16 + h * 8;
 #pragma unroll
-        for (int s = 0; s < KW; ++s) {
-          if (!(ALL || ((am >> s) & 1u))) continue;
-          T* tp = tb + (int64_t)(ka[s] >> 5) * 1024;
+          for (int pr = 0; pr < NPAIR; ++pr) {
+            T* tb = (T*)(pr == 0 ? p.dstile : p.dstile2) + toff;
 #pragma unroll
-          for (int c2 = 0; c2 < NC2; ++c2) __builtin_nontemporal_store(dso[0][s][c2], (Op*)(tp + 512 * c2));
+            for (int s = 0; s < KW; ++s) {
+              if (!(ALL || ((am >> s) & 1u))) continue;
+              T* tp = tb + (int64_t)(ka[s] >> 5) * 1024;
+#pragma unroll
+              for (int c2 = 0; c2 < NC2; ++c2) __builtin_nontemporal_store(dso[pr][s][c2], (Op*)(tp + 512 * c2));
+            }
+          }
         }
       }
-    }
+    };
+    constexpr bool DS_MID = POLY == POLY_GEN2;
     if constexpr (WANT_DV) {
 #pragma unroll
       for (int d = 0; d < NDV; ++d)
@@ -1181,6 +1190,7 @@ k_bwd_kv(const KParams p) {
             if (ALL || ((am >> s) & 1u)) dv[s][d] = M::mma(a, po[s][c2], dv[s][d]);
         }
     }
+    if constexpr (DS_MID) store_ds();
     if constexpr (WANT_DK) {
 #pragma unroll
       for (int pr = 0; pr < NPAIR; ++pr)
@@ -1194,6 +1204,7 @@ k_bwd_kv(const KParams p) {
               if (ALL || ((am >> s) & 1u)) dk[pr][s][d] = M::mma(a, dso[pr][s][c2], dk[pr][s][d]);
           }
     }
+    if constexpr (!DS_MID) store_ds();
   };
 
   auto step = [&](const int m, auto fast_c) {

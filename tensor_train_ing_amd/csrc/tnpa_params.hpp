@@ -31,7 +31,8 @@ struct KParams {
   const float* offs;   // (H) offset_square offsets or null
   float* norms;        // (NPAIR, 2, H) max row norms of q and k (forward), or null
   float* dpar;         // (B*H, NNB, 4) per-key-block partial sums for dcoef / db, or null
-  void* dstile;        // dS tiles written by the dK pass and read by the dQ-from-dS kernel, or null (see ds_tile_*)
+  void* dstile;        // dS tiles written by the key side and read by the dQ-from-dS kernel, or null (see ds_tile_*)
+  void* dstile2;       // the same for the second q/k pair (dS2), or null
   int dpre;            // 1: dsc holds the row-scaled dout; 0: the dK/dV pass scales dout while staging it
   int kvsel;           // key-side kernels to launch: 1 = dV pass, 2 = dK pass, 3 = both (or the combined kernel)
   int B, H, T;

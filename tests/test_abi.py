@@ -165,6 +165,13 @@ def test_backward_workspace_size(lib):
     # lower_degree_mix (two pairs) streams the row-scaled dO: partials, then (B, H, T, dv) bf16
     p = _problem(kind=_abi.LOWER_DEGREE_MIX, coef=4096, seq_len=300)
     assert lib.tnpa_backward_workspace_bytes(ctypes.byref(p)) == r(2 * 2 * 3 * 4 * 4) + r(2 * 2 * 300 * 64 * 2)
+    # at key head dim 128 the two-pair kinds add one set of dS tiles per pair (dS1, dS2)
+    p = _problem(kind=_abi.LOWER_DEGREE_MIX, coef=4096, seq_len=300, head_dim_k=128, head_dim_v=128)
+    assert lib.tnpa_backward_workspace_bytes(ctypes.byref(p)) == (r(2 * 2 * 3 * 4 * 4) + r(2 * 2 * 300 * 128 * 2)
+                                                                   + 2 * r(2 * 2 * tiles * 1024 * 2))
+    assert lib.tnpa_x_workspace_bytes(ctypes.byref(p), _abi.X_DS_OFF) == r(2 * 2 * 3 * 4 * 4) + r(2 * 2 * 300 * 128 * 2)
+    p = _problem(kind=_abi.SIGNED_PRODUCT, seq_len=300, head_dim_k=128, head_dim_v=64)
+    assert lib.tnpa_backward_workspace_bytes(ctypes.byref(p)) == r(2 * 2 * 300 * 64 * 2) + 2 * r(2 * 2 * tiles * 1024 * 2)
     # forcing the row-scaled dO on or off changes only that part
     p = _problem()
     assert lib.tnpa_x_workspace_bytes(ctypes.byref(p), _abi.X_PRESCALE_ON) == r(2 * 2 * 128 * 64 * 2)
@@ -182,8 +189,8 @@ def test_backward_plan(lib):
     """Which launches tnpa_backward makes: the row-scaled dO only where the key side cannot scale dO for free (fp32,
     two q/k pairs, or a head dim too small for the three-buffer tile split); separate dV and dK passes for 16-bit one
     q/k pair at a head dim above 64, except head dims 128 / 128, whose key side is the one wave-pair kernel; dQ from
-    the dS tiles at key head dim 128 (dQ recomputing S and dP otherwise, or with X_DS_OFF); the dpar reduction for
-    the kinds with head parameters."""
+    the dS tiles at key head dim 128 for 16-bit inputs, one pair or two (dQ recomputing S and dP otherwise, or with
+    X_DS_OFF); the dpar reduction for the kinds with head parameters."""
     from tensor_train_ing_amd import _abi
     assert _launches(lib, _problem()) == ["kv", "q"]
     assert _launches(lib, _problem(head_dim_k=128, head_dim_v=128)) == ["kv", "qds"]
@@ -198,6 +205,13 @@ def test_backward_plan(lib):
     assert _launches(lib, _problem(head_dim_v=32)) == ["kv", "q"]
     assert _launches(lib, _problem(kind=_abi.OFFSET_SQUARE, offset=4096)) == ["kv", "q", "dpar"]
     assert _launches(lib, _problem(kind=_abi.LOWER_DEGREE_MIX, coef=4096)) == ["scale", "kv", "q", "dpar"]
+    assert _launches(lib, _problem(kind=_abi.SIGNED_PRODUCT, head_dim_k=128, head_dim_v=128)) == ["scale", "kv", "qds"]
+    assert _launches(lib, _problem(kind=_abi.LOWER_DEGREE_MIX, coef=4096, head_dim_k=128, head_dim_v=64)) == [
+        "scale", "kv", "qds", "dpar"]
+    assert _launches(lib, _problem(kind=_abi.SIGNED_PRODUCT, head_dim_k=128, head_dim_v=128), _abi.X_DS_OFF) == [
+        "scale", "kv", "q"]
+    assert _launches(lib, _problem(kind=_abi.SIGNED_PRODUCT, dtype=_abi.F32, head_dim_k=128, head_dim_v=128)) == [
+        "scale", "kv", "q"]
     assert _launches(lib, _problem(), _abi.X_PRESCALE_ON) == ["scale", "kv", "q"]
     assert _launches(lib, _problem(dtype=_abi.F32), _abi.X_PRESCALE_OFF) == ["kv", "q"]
     assert lib.tnpa_x_launch_name(ctypes.byref(_problem()), 0, 5) == b""

@@ -512,6 +512,47 @@ def test_dq_from_ds_tiles_matches_recompute(degree, dtype, T, docs):
         assert rel_fro(o["dq1"], ref["dq1"]) < BF16_FRO and rel_max(o["dq1"], ref["dq1"]) < BF16_MAX
 
 
+@pytest.mark.parametrize("kind,T,docs", [("signed_product", 300, True), ("signed_product", 77, False),
+                                         ("lower_degree_mix", 333, True), ("lower_degree_mix", 512, False)])
+def test_two_pair_dq_from_ds_tiles_matches_recompute(kind, T, docs):
+    """Head dim 128, bf16, two q/k pairs: the combined key-side kernel stores dS1 and dS2 as tiles and dQ1 = dS1 K1,
+    dQ2 = dS2 K2 come from them ("qds", two launches of the dQ-from-dS kernel); X_DS_OFF recomputes S1, S2 and dP
+    in the dQ kernel ("q"). dK1, dK2, dV and dcoef come from the same kernel (bit-identical); dQ1 and dQ2 differ only
+    in rounding inside the products (relative Frobenius < 5e-3), and both meet the bf16 tolerance of the float64
+    reference."""
+    from tensor_train_ing_amd import _abi
+    from tensor_train_ing_amd.poly_attn import KINDS, _problem, _stream, doc_bounds
+    print(f"[two-pair qds] kind={kind} T={T} docs={docs}", flush=True)
+    B, H, D = 2, 3, 128
+    q1, k1, q2, k2, v, dout = (x.cuda() for x in gaussian_inputs(B, H, T, D, D, torch.bfloat16, 23,
+                                                                  qk_scale=D ** -0.25, two_pairs=True))
+    dk_ = _doc_rows(B, T).cuda() if docs else torch.zeros(B, T, dtype=torch.long, device="cuda")
+    rs = row_scale(dk_, 0.5).float().contiguous()
+    dstart, qend = doc_bounds(dk_)
+    coef = torch.tensor([[0.3, -0.5, 0.7, 1.1]], device="cuda").repeat(H, 1).contiguous()
+    cf = coef if kind == "lower_degree_mix" else None
+    prob = _problem(KINDS[kind], 0, q1, k1, q2, k2, v, dstart, qend, rs, cf, None)
+    lib = _abi.load()
+    names = [lib.tnpa_x_launch_name(ctypes.byref(prob), 0, i).decode() for i in range(lib.tnpa_x_launches(
+        ctypes.byref(prob), 0))]
+    assert names == ["scale", "kv", "qds"] + (["dpar"] if cf is not None else []), names
+    outs = []
+    for opts in (0, _abi.X_DS_OFF):
+        g, bufs, ws = _grads(lib, prob, opts, dout, k1, v, H, True, q1)
+        ws.fill_(0xFF)  # stale bytes: NaN-like bf16 patterns where a tile was never written
+        _abi.check(lib.tnpa_x_backward(ctypes.byref(prob), ctypes.byref(g), opts, -1, _stream(q1.device)), "bwd")
+        torch.cuda.synchronize()
+        outs.append(bufs)
+    for n in ("dk1", "dk2", "dv") + (("dpar",) if cf is not None else ()):
+        assert torch.equal(outs[0][n], outs[1][n]), n
+    ref = dense_reference(kind, q1, k1, q2, k2, v, dout, dk_, rs, cf)
+    for n in ("dq1", "dq2"):
+        assert torch.isfinite(outs[0][n]).all(), n
+        assert rel_fro(outs[0][n], outs[1][n]) < 5e-3, n
+        for o in outs:
+            assert rel_fro(o[n], ref[n]) < BF16_FRO and rel_max(o[n], ref[n]) < BF16_MAX, n
+
+
 # ------------------------------------------------------------------ BASELINE.json configurations, full size
 BASELINE_CONFIGS = {
     "100m_b16h12t1024d64_p2": dict(B=16, H=12, T=1024, D=64, degree=2, boost=0.0),
