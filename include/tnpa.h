@@ -24,7 +24,7 @@
 extern "C" {
 #endif
 
-#define TNPA_ABI_VERSION 3
+#define TNPA_ABI_VERSION 4
 
 typedef enum {
   TNPA_OK = 0,
@@ -54,7 +54,12 @@ typedef struct {
  * max over (b, t) of the Euclidean norm of q_pair[b,h,t,:] ([pair][0][h]) and of k_pair[b,h,t,:] ([pair][1][h]),
  * over every token (padding included), pairs = 2 for signed_product / lower_degree_mix and 1 otherwise: the two
  * factors of the reference's Cauchy-Schwarz score bound max|S| <= max|q| max|k| / sqrt(dk)
- * (ref: tnlm/model.py:33-38,83-85), taken from the rows the forward kernel reads anyway. */
+ * (ref: tnlm/model.py:33-38,83-85), taken from the rows the forward kernel reads anyway.
+ * rope_cos / rope_sin (optional, both or neither): per-token rotary tables, (B, T, dk/2) fp32 contiguous, as the
+ * reference's rope_tables builds them (ref: tnlm/attention.py:41-45; its (B, 1, T, dk/2) layout is the same memory).
+ * With them, q1/k1 (q2/k2) are the inputs already rotated by these tables (tnpa_rope), tnpa_forward is unchanged,
+ * and tnpa_backward returns dq/dk with respect to the unrotated inputs: the gradient of the rotation is applied to
+ * them in the library (ref: tnlm/attention.py:48-51 and its autograd), so the caller runs no pass of its own. */
 typedef struct {
   int32_t batch, heads, seq_len, head_dim_k, head_dim_v;
   int32_t kind;   /* tnpa_kind */
@@ -67,6 +72,8 @@ typedef struct {
   const float* coef;
   const float* offset;
   float* score_norms;
+  const float* rope_cos;
+  const float* rope_sin;
 } tnpa_problem_t;
 
 /* Gradients for tnpa_backward. dout is dL/dy (B,H,T,dv). dq2/dk2 are ignored for one-pair kinds. dpar is an (H,4)
@@ -97,6 +104,16 @@ const char* tnpa_last_error(void);
  * ref: tnlm/attention.py:12-19 (doc_positions); ids must be contiguous runs, negative = padding. */
 int tnpa_doc_bounds(const void* doc_ids, int32_t doc_is_int64, int64_t doc_stride_b, int32_t batch,
                     int32_t seq_len, int32_t* doc_start, int32_t* query_end, void* stream);
+
+/* Rotary position embedding of one (B,H,T,d) tensor x into out (same shape and dtype; out may be x itself) by
+ * per-token tables cos / sin, (B, T, d/2) fp32 contiguous (ref: tnlm/attention.py:41-45). One pass, in fp32 with
+ * x1 = x[..., :d/2], x2 = x[..., d/2:]: inverse = 0 gives out = (x1 cos - x2 sin, x1 sin + x2 cos), the reference's
+ * apply_rope (ref: tnlm/attention.py:48-51, called at ref: tnlm/model.py:70-71,81-82); inverse = 1 gives the
+ * gradient of that rotation with respect to its input, g -> (g1 cos + g2 sin, g2 cos - g1 sin). Every product and
+ * sum is rounded to fp32 on its own and the result to the dtype, bit-identical to the reference's tensor
+ * operations and their autograd. tnpa_backward applies the inverse itself when the problem carries the tables. */
+int tnpa_rope(const tnpa_tensor_t* x, const tnpa_tensor_t* out, int32_t batch, int32_t heads, int32_t seq_len,
+              int32_t head_dim, int32_t dtype, const float* cos, const float* sin, int32_t inverse, void* stream);
 
 /* Forward: writes out (B,H,T,dv) in the problem dtype. Replaces ref: tnlm/kernels/poly_attn.py:271-280
  * (PolyAttention.forward launch of _fwd). */

@@ -12,7 +12,7 @@ import os
 from pathlib import Path
 
 LIB_PATH = Path(__file__).resolve().parent / "libtnpa.so"
-ABI_VERSION = 3
+ABI_VERSION = 4
 
 OK, ERR_INVALID, ERR_UNSUPPORTED, ERR_LAUNCH = 0, 1, 2, 3
 BF16, F32, F16 = 0, 1, 2
@@ -33,7 +33,8 @@ class Problem(ctypes.Structure):
                 ("degree", ctypes.c_int32), ("dtype", ctypes.c_int32),
                 ("q1", Tensor), ("k1", Tensor), ("q2", Tensor), ("k2", Tensor), ("v", Tensor),
                 ("doc_start", ctypes.c_void_p), ("query_end", ctypes.c_void_p), ("row_scale", ctypes.c_void_p),
-                ("coef", ctypes.c_void_p), ("offset", ctypes.c_void_p), ("score_norms", ctypes.c_void_p)]
+                ("coef", ctypes.c_void_p), ("offset", ctypes.c_void_p), ("score_norms", ctypes.c_void_p),
+                ("rope_cos", ctypes.c_void_p), ("rope_sin", ctypes.c_void_p)]
 
 
 class Grads(ctypes.Structure):
@@ -50,6 +51,9 @@ _SIGNATURES = {
     "tnpa_doc_bounds": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_int32, ctypes.c_int64, ctypes.c_int32,
                                        ctypes.c_int32, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p]),
     "tnpa_forward": (ctypes.c_int, [ctypes.POINTER(Problem), ctypes.POINTER(Tensor), ctypes.c_void_p]),
+    "tnpa_rope": (ctypes.c_int, [ctypes.POINTER(Tensor), ctypes.POINTER(Tensor), ctypes.c_int32, ctypes.c_int32,
+                                 ctypes.c_int32, ctypes.c_int32, ctypes.c_int32, ctypes.c_void_p, ctypes.c_void_p,
+                                 ctypes.c_int32, ctypes.c_void_p]),
     "tnpa_backward_workspace_bytes": (ctypes.c_int64, [ctypes.POINTER(Problem)]),
     "tnpa_backward": (ctypes.c_int, [ctypes.POINTER(Problem), ctypes.POINTER(Grads), ctypes.c_void_p]),
     "tnpa_backward_noalloc": (ctypes.c_int, [ctypes.POINTER(Problem), ctypes.POINTER(Grads), ctypes.c_void_p]),

@@ -103,6 +103,8 @@ int check_problem(const tnpa_problem_t* pp) {
     return fail(TNPA_ERR_INVALID, "lower_degree_mix needs coef (H,4)");
   if (p.kind == TNPA_OFFSET_SQUARE && p.offset == nullptr)
     return fail(TNPA_ERR_INVALID, "offset_square needs offset (H)");
+  if ((p.rope_cos == nullptr) != (p.rope_sin == nullptr))
+    return fail(TNPA_ERR_INVALID, "rope_cos and rope_sin: both or neither");
   return TNPA_OK;
 }
 
@@ -344,6 +346,82 @@ hipError_t scale_rows(const tnpa_problem_t& p, const tnpa_tensor_t& d, const tnp
   return hipGetLastError();
 }
 
+// Rotary position embedding of a (B, H, T, d) tensor by per-token tables cos / sin, (B, T, d/2) fp32
+// (ref: tnlm/attention.py:48-51): x1 = x[..., :d/2], x2 = x[..., d/2:] in fp32;
+//   forward: out = (x1 cos - x2 sin, x1 sin + x2 cos);
+//   INV, the gradient of the forward as autograd forms it from g = dL/dout: (g1 cos + g2 sin, g2 cos - g1 sin).
+// Every product and sum is rounded to fp32 on its own (no fused multiply-add: the reference runs them as separate
+// tensor operations), then rounded to T. One thread per 16-byte chunk of x1 with the matching chunk of x2
+// (grid-stride); out may be x itself.
+template <typename T, bool INV>
+__global__ void __launch_bounds__(256) k_rope(const T* x, int64_t sb, int64_t sh, int64_t st, T* out, int64_t ob,
+                                              int64_t oh, int64_t ot, const float* __restrict__ cs,
+                                              const float* __restrict__ sn, int B, int H, int T_, int D) {
+#pragma clang fp contract(off)
+  typedef unsigned int u4 __attribute__((ext_vector_type(4)));
+  typedef float f4 __attribute__((ext_vector_type(4)));
+  constexpr int CE = 16 / (int)sizeof(T);
+  const int half = D / 2, nch = half / CE;
+  const int64_t total = (int64_t)B * H * T_ * nch;
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total; i += (int64_t)gridDim.x * blockDim.x) {
+    const int c = (int)(i % nch);
+    const int64_t row = i / nch;
+    const int t = (int)(row % T_);
+    const int64_t bh = row / T_;
+    const int h = (int)(bh % H), b = (int)(bh / H);
+    const T* xr = x + b * sb + h * sh + t * st + c * CE;
+    u4 r1 = *(const u4*)xr, r2 = *(const u4*)(xr + half);
+    const int64_t tab = ((int64_t)b * T_ + t) * half + c * CE;
+    float cv[CE], sv[CE];
+#pragma unroll
+    for (int j = 0; j < CE; j += 4) {
+      const f4 a = *(const f4*)(cs + tab + j), z = *(const f4*)(sn + tab + j);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        cv[j + e] = a[e];
+        sv[j + e] = z[e];
+      }
+    }
+    T* e1 = reinterpret_cast<T*>(&r1);
+    T* e2 = reinterpret_cast<T*>(&r2);
+#pragma unroll
+    for (int j = 0; j < CE; ++j) {
+      const float a = (float)e1[j], z = (float)e2[j];
+      const float p1 = a * cv[j], p2 = z * sv[j], p3 = a * sv[j], p4 = z * cv[j];
+      if constexpr (INV) {
+        e1[j] = (T)(p1 + p2);
+        e2[j] = (T)(p4 - p3);
+      } else {
+        e1[j] = (T)(p1 - p2);
+        e2[j] = (T)(p3 + p4);
+      }
+    }
+    T* orow = out + b * ob + h * oh + t * ot + c * CE;
+    *(u4*)orow = r1;
+    *(u4*)(orow + half) = r2;
+  }
+}
+
+template <typename T, bool INV>
+hipError_t rope_rows(const tnpa_problem_t& p, const tnpa_tensor_t& x, const tnpa_tensor_t& o, hipStream_t s) {
+  const int CE = 16 / (int)sizeof(T);
+  const int64_t total = (int64_t)p.batch * p.heads * p.seq_len * (p.head_dim_k / 2 / CE);
+  const int grid = (int)std::min<int64_t>((total + 255) / 256, 8192);
+  hipLaunchKernelGGL((k_rope<T, INV>), dim3(grid), dim3(256), 0, s, (const T*)x.data, x.stride_b, x.stride_h,
+                     x.stride_t, (T*)o.data, o.stride_b, o.stride_h, o.stride_t, p.rope_cos, p.rope_sin, p.batch,
+                     p.heads, p.seq_len, p.head_dim_k);
+  return hipGetLastError();
+}
+
+template <bool INV>
+hipError_t rope_any(const tnpa_problem_t& p, const tnpa_tensor_t& x, const tnpa_tensor_t& o, hipStream_t s) {
+  switch (p.dtype) {
+    case TNPA_BF16: return rope_rows<__bf16, INV>(p, x, o, s);
+    case TNPA_F16: return rope_rows<_Float16, INV>(p, x, o, s);
+    default: return rope_rows<float, INV>(p, x, o, s);
+  }
+}
+
 // dpar[h, c] = sum over (b, key block) of the per-block partials, in a fixed order.
 // ref: tnlm/kernels/poly_attn.py:304 (dpar.view(B, H, NB, 4).sum((0, 2)))
 __global__ void k_dpar_reduce(const float* part, int B, int H, int NNB, float* out) {
@@ -365,8 +443,8 @@ __global__ void k_dpar_reduce(const float* part, int B, int H, int NNB, float* o
 //   qds    dQ = dS K from the dS tiles the dk pass stored in the workspace (16-bit, one q/k pair, head dim 128,
 //          unless TNPA_X_DS_OFF or the tiles would exceed kMaxDsTileBytes): one matrix product instead of three
 //   dpar   the fixed-order dcoef/db reduction of the per-key-block partials (offset_square, lower_degree_mix)
-enum LaunchKind { L_SCALE = 0, L_KV = 1, L_DV = 2, L_DK = 3, L_Q = 4, L_DPAR = 5, L_QDS = 6 };
-const char* const kLaunchNames[] = {"scale", "kv", "dv", "dk", "q", "dpar", "qds"};
+enum LaunchKind { L_SCALE = 0, L_KV = 1, L_DV = 2, L_DK = 3, L_Q = 4, L_DPAR = 5, L_QDS = 6, L_ROPE = 7 };
+const char* const kLaunchNames[] = {"scale", "kv", "dv", "dk", "q", "dpar", "qds", "rope"};
 
 // Largest dS tile area the plan uses (B * H * T^2 bytes for 16-bit inputs, 545 MB at B8 H16 T2048); larger problems
 // recompute S and dP in the dQ kernel instead.
@@ -374,7 +452,7 @@ constexpr int64_t kMaxDsTileBytes = 4LL << 30;
 
 struct Plan {
   int n = 0;
-  int what[6] = {0, 0, 0, 0, 0, 0};
+  int what[7] = {0, 0, 0, 0, 0, 0, 0};
   bool prescale = false, par = false, ds = false;
   int nnb = 0;  // key blocks per row (dpar partials)
   int64_t dpar_off = 0, dos_off = 0, ds_off = 0, ds2_off = 0, bytes = 0;
@@ -417,6 +495,7 @@ int make_plan(const tnpa_problem_t& p, int opts, Plan& pl) {
   }
   pl.what[pl.n++] = pl.ds ? L_QDS : L_Q;
   if (pl.par) pl.what[pl.n++] = L_DPAR;
+  if (p.rope_cos != nullptr) pl.what[pl.n++] = L_ROPE;
   return TNPA_OK;
 }
 
@@ -489,6 +568,13 @@ int run_backward(const tnpa_problem_t* problem, const tnpa_grads_t* grads, int o
                                    : tnpa::launch_bwd_q_ds<_Float16, 128>(pr ? k2 : k, stream);
         break;
       }
+      case L_ROPE:
+        // the gradient of the caller's rotation, in place on dq and dk
+        e = rope_any<true>(p, grads->dq1, grads->dq1, stream);
+        if (e == hipSuccess) e = rope_any<true>(p, grads->dk1, grads->dk1, stream);
+        if (two_pairs(p.kind) && e == hipSuccess) e = rope_any<true>(p, grads->dq2, grads->dq2, stream);
+        if (two_pairs(p.kind) && e == hipSuccess) e = rope_any<true>(p, grads->dk2, grads->dk2, stream);
+        break;
       case L_DPAR: {
         const int n = p.heads * 4;
         hipLaunchKernelGGL(k_dpar_reduce, dim3((n + 255) / 256), dim3(256), 0, stream, (const float*)k.dpar, p.batch,
@@ -555,6 +641,31 @@ int tnpa_doc_bounds(const void* doc_ids, int32_t doc_is_int64, int64_t doc_strid
                      doc_stride_b, seq_len, doc_start, query_end);
   const hipError_t e = hipGetLastError();
   if (e != hipSuccess) return fail(TNPA_ERR_LAUNCH, "tnpa_doc_bounds: %s", hipGetErrorString(e));
+  return ok();
+}
+
+int tnpa_rope(const tnpa_tensor_t* x, const tnpa_tensor_t* out, int32_t batch, int32_t heads, int32_t seq_len,
+              int32_t head_dim, int32_t dtype, const float* cos, const float* sin, int32_t inverse, void* stream) {
+  if (x == nullptr || out == nullptr || cos == nullptr || sin == nullptr)
+    return fail(TNPA_ERR_INVALID, "tnpa_rope: null pointer");
+  if (batch <= 0 || heads <= 0 || seq_len <= 0) return fail(TNPA_ERR_INVALID, "tnpa_rope: sizes must be positive");
+  if (!valid_dim(head_dim)) return fail(TNPA_ERR_INVALID, "tnpa_rope: head dim must be a power of 2 >= 16");
+  if (dtype != TNPA_BF16 && dtype != TNPA_F32 && dtype != TNPA_F16)
+    return fail(TNPA_ERR_INVALID, "tnpa_rope: unknown dtype %d", dtype);
+  tnpa_problem_t p{};
+  p.batch = batch;
+  p.heads = heads;
+  p.seq_len = seq_len;
+  p.head_dim_k = head_dim;
+  p.dtype = dtype;
+  p.rope_cos = cos;
+  p.rope_sin = sin;
+  const int es = esize(dtype);
+  int rc;
+  if ((rc = check_tensor(*x, "x", p, es)) || (rc = check_tensor(*out, "out", p, es))) return rc;
+  const hipError_t e = inverse ? rope_any<true>(p, *x, *out, (hipStream_t)stream)
+                               : rope_any<false>(p, *x, *out, (hipStream_t)stream);
+  if (e != hipSuccess) return fail(TNPA_ERR_LAUNCH, "tnpa_rope: %s", hipGetErrorString(e));
   return ok();
 }
 

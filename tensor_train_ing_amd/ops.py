@@ -9,6 +9,7 @@ implementations and an autograd formula:
                                     want_norms) -> (o, score_norms)   (score_norms empty unless want_norms)
     tnpa::poly_attention_backward  (kind, degree, q1, k1, q2?, k2?, v, doc_start, query_end, row_scale, coef?, b?, dO)
                                    -> (dq1, dk1, dq2, dk2, dv, dpar)
+    tnpa::rope                     (x, cos, sin, inverse) -> rotated x   (its gradient: the same op, inverted)
 
 Outputs and gradients are contiguous (B, H, T, d); dq2/dk2 are empty for one-pair kinds and dpar is empty unless the
 kind has head parameters. The document bounds are an input of the attention op: computed once per batch by a model
@@ -21,7 +22,7 @@ from typing import Optional
 import torch
 
 from . import _abi
-from .poly_attn import _canonical, _prep, _run_backward, _run_forward, doc_bounds
+from .poly_attn import _canonical, _prep, _run_backward, _run_forward, doc_bounds, rope_rotate, rope_tables_of
 
 _PAR_KINDS = (_abi.OFFSET_SQUARE, _abi.LOWER_DEGREE_MIX)
 _TWO_PAIRS = (_abi.SIGNED_PRODUCT, _abi.LOWER_DEGREE_MIX)
@@ -36,6 +37,30 @@ def doc_bounds_op(doc_ids: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
 def _bounds_fake(doc_ids):
     B, T = doc_ids.shape
     return doc_ids.new_empty((B, T), dtype=torch.int32), doc_ids.new_empty((B, T), dtype=torch.int32)
+
+
+@torch.library.custom_op("tnpa::rope", mutates_args=())
+def rope_op(x: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor, inverse: bool) -> torch.Tensor:
+    return rope_rotate(x, cos, sin, inverse)
+
+
+@rope_op.register_fake
+def _rope_fake(x, cos, sin, inverse):
+    return x.new_empty(x.shape)
+
+
+def _rope_setup(ctx, inputs, output):
+    _x, cos, sin, inverse = inputs
+    ctx.inverse = inverse
+    ctx.save_for_backward(cos, sin)
+
+
+def _rope_backward(ctx, g):
+    cos, sin = ctx.saved_tensors
+    return rope_op(g.contiguous(), cos, sin, not ctx.inverse), None, None, None
+
+
+rope_op.register_autograd(_rope_backward, setup_context=_rope_setup)
 
 
 def _norms_shape(kind, H, want):
@@ -110,11 +135,17 @@ _fwd.register_autograd(_backward, setup_context=_setup_context)
 
 
 def poly_attention_op(kind, q1, k1, q2, k2, v, doc_ids, row_scale, coef=None, b=None, *, degree=None, bounds=None,
-                      score_norms=None):
+                      score_norms=None, rope=None):
     """poly_attention_hip through the registered custom ops (same arguments, same results; contiguous output).
-    Unknown kinds raise KeyError, as the reference."""
+    Unknown kinds raise KeyError, as the reference. With rotary tables, q/k are rotated by tnpa::rope (whose
+    gradient is the inverse rotation, the same arithmetic the eager backward applies in the library)."""
     K, degree = _canonical(kind, q1, k1, q2, k2, degree)
     two = K in _TWO_PAIRS
+    if rope is not None:
+        cs, sn = rope_tables_of(rope, q1)
+        q1, k1 = rope_op(q1, cs, sn, False), rope_op(k1, cs, sn, False)
+        if two:
+            q2, k2 = rope_op(q2, cs, sn, False), rope_op(k2, cs, sn, False)
     dstart, qend = doc_bounds_op(doc_ids) if bounds is None else bounds
     o, norms = _fwd(K, int(degree) if degree is not None else 0, q1, k1, q2 if two else None, k2 if two else None,
                     v, dstart, qend, row_scale, coef if K == _abi.LOWER_DEGREE_MIX else None,

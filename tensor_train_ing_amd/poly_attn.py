@@ -83,6 +83,42 @@ def doc_bounds(doc_ids: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
     return dstart, qend
 
 
+def rope_tables_of(rope, q1: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
+    """(cos, sin) as the kernels read them: fp32 (B, T, dk/2) contiguous, from the reference's rope_tables layout
+    (B, 1, T, dk/2) or from (B, T, dk/2) (ref: tnlm/attention.py:41-45)."""
+    if not (isinstance(rope, (tuple, list)) and len(rope) == 2):
+        raise ValueError("rope must be the (cos, sin) pair of rotary tables")
+    B, _, T, DK = q1.shape
+    out = []
+    for name, t in zip(("cos", "sin"), rope):
+        if t.dim() == 4 and t.shape[1] == 1:
+            t = t[:, 0]
+        if tuple(t.shape) != (B, T, DK // 2):
+            raise ValueError(f"rope {name}: shape {tuple(t.shape)}, expected {(B, T, DK // 2)} or {(B, 1, T, DK // 2)}")
+        if t.device != q1.device:
+            raise ValueError(f"rope {name} must be on the same device as q1")
+        if t.requires_grad and torch.is_grad_enabled():
+            raise ValueError("rope tables are fixed position-only factors; differentiable tables are not supported")
+        out.append(t.detach().float().contiguous())
+    return out[0], out[1]
+
+
+def rope_rotate(x: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor, inverse: bool = False,
+                out: torch.Tensor = None) -> torch.Tensor:
+    """One-pass rotary embedding of a (B, H, T, d) tensor (tnpa_rope): the reference's apply_rope
+    (ref: tnlm/attention.py:48-51), bit-identical, or with inverse=True the gradient of that rotation. cos / sin as
+    rope_tables_of returns them. Writes `out` (a new tensor by default; may be x)."""
+    x = _prep(x)
+    out = torch.empty(x.shape, dtype=x.dtype, device=x.device) if out is None else out
+    B, H, T, D = x.shape
+    lib = _abi.load()
+    with torch.cuda.device(x.device):
+        _abi.check(lib.tnpa_rope(ctypes.byref(_desc(x)), ctypes.byref(_desc(out)), B, H, T, D, _DTYPES[x.dtype],
+                                 ctypes.c_void_p(cos.data_ptr()), ctypes.c_void_p(sin.data_ptr()), int(inverse),
+                                 _stream(x.device)), "rope")
+    return out
+
+
 def _validate(K, q1, k1, q2, k2, v, doc_ids, row_scale, coef, b, degree):
     if q1.dim() != 4 or v.dim() != 4:
         raise ValueError("q*, k*, v must be (B, H, T, d)")
@@ -139,15 +175,20 @@ def _check_bounds(bounds, doc_ids):
 
 
 def _run_forward(K, degree, q1, k1, q2, k2, v, doc_ids, row_scale, coef, b, out_like_v=True, bounds=None,
-                 score_norms=None):
-    """Validates, computes the document bounds (unless given) and launches the forward. Returns (o, dstart, qend,
-    (q1, k1, q2, k2, v) as the kernels read them, sc, coef_f, b_f). o has v's strides (out_like_v) or is
-    contiguous."""
+                 score_norms=None, rope=None):
+    """Validates, computes the document bounds (unless given), rotates q/k by the rotary tables (if given) and
+    launches the forward. Returns (o, dstart, qend, (q1, k1, q2, k2, v) as the kernels read them (rotated), sc,
+    coef_f, b_f). o has v's strides (out_like_v) or is contiguous."""
     _validate(K, q1, k1, q2, k2, v, doc_ids, row_scale, coef, b, degree)
     q1, k1, v = _prep(q1), _prep(k1), _prep(v)
     if K in _TWO_PAIRS:
         q2, k2 = _prep(q2), _prep(k2)
-    else:
+    if rope is not None:
+        cs, sn = rope
+        q1, k1 = rope_rotate(q1, cs, sn), rope_rotate(k1, cs, sn)
+        if K in _TWO_PAIRS:
+            q2, k2 = rope_rotate(q2, cs, sn), rope_rotate(k2, cs, sn)
+    if K not in _TWO_PAIRS:
         q2, k2 = q1, k1
     dstart, qend = doc_bounds(doc_ids) if bounds is None else _check_bounds(bounds, doc_ids)
     sc = row_scale.detach().float().contiguous()
@@ -161,7 +202,7 @@ def _run_forward(K, degree, q1, k1, q2, k2, v, doc_ids, row_scale, coef, b, out_
         if (score_norms.dtype != torch.float32 or tuple(score_norms.shape) != (pairs, 2, q1.shape[1])
                 or not score_norms.is_contiguous() or score_norms.device != q1.device):
             raise ValueError(f"score_norms must be a contiguous float32 ({pairs}, 2, H) tensor on q1's device")
-    prob = _problem(K, degree, q1, k1, q2, k2, v, dstart, qend, sc, coef_f, b_f, score_norms)
+    prob = _problem(K, degree, q1, k1, q2, k2, v, dstart, qend, sc, coef_f, b_f, score_norms, rope)
     lib = _abi.load()
     with torch.cuda.device(q1.device):
         _abi.check(lib.tnpa_forward(ctypes.byref(prob), ctypes.byref(_desc(o)), _stream(q1.device)),
@@ -169,16 +210,18 @@ def _run_forward(K, degree, q1, k1, q2, k2, v, doc_ids, row_scale, coef, b, out_
     return o, dstart, qend, (q1, k1, q2, k2, v), sc, coef_f, b_f
 
 
-def _run_backward(K, degree, q1, k1, q2, k2, v, dstart, qend, sc, coef_f, b_f, do, grads_like_inputs=True):
+def _run_backward(K, degree, q1, k1, q2, k2, v, dstart, qend, sc, coef_f, b_f, do, grads_like_inputs=True,
+                  rope=None):
     """Launches the backward on tensors prepared by _run_forward. Returns (dq1, dk1, dq2, dk2, dv, dpar), with
-    dq2/dk2 None for one-pair kinds and dpar the (H, 4) fp32 head-parameter gradient or None."""
+    dq2/dk2 None for one-pair kinds and dpar the (H, 4) fp32 head-parameter gradient or None. With the rotary tables
+    (q/k then being the rotated tensors) dq/dk are with respect to the unrotated q/k."""
     H = q1.shape[1]
     do = _prep(do.to(v.dtype))
     alloc = _alloc_like if grads_like_inputs else (lambda x: torch.empty(x.shape, dtype=x.dtype, device=x.device))
     dq1, dk1, dv = alloc(q1), alloc(k1), alloc(v)
     two = K in _TWO_PAIRS
     dq2, dk2 = (alloc(q2), alloc(k2)) if two else (dq1, dk1)
-    prob = _problem(K, degree, q1, k1, q2, k2, v, dstart, qend, sc, coef_f, b_f)
+    prob = _problem(K, degree, q1, k1, q2, k2, v, dstart, qend, sc, coef_f, b_f, rope=rope)
     lib = _abi.load()
     par = K in (_abi.OFFSET_SQUARE, _abi.LOWER_DEGREE_MIX)
     dpar = torch.empty(H, 4, dtype=torch.float32, device=q1.device) if par else None
@@ -202,12 +245,15 @@ class PolyAttention(torch.autograd.Function):
 
     @staticmethod
     def forward(ctx, kind, q1, k1, q2, k2, v, doc_ids, row_scale, coef, b, degree=None, bounds=None,
-                score_norms=None):
+                score_norms=None, rope=None):
         shared = KINDS[kind] == _abi.SIGNED_PRODUCT and q2 is q1 and k2 is k1
         K, degree = _canonical(kind, q1, k1, q2, k2, degree)
+        tabs = rope_tables_of(rope, q1) if rope is not None else None
         o, dstart, qend, (q1, k1, q2, k2, v), sc, coef_f, b_f = _run_forward(
-            K, degree, q1, k1, q2, k2, v, doc_ids, row_scale, coef, b, bounds=bounds, score_norms=score_norms)
-        ctx.save_for_backward(q1, k1, q2, k2, v, dstart, qend, sc, coef_f, b_f)
+            K, degree, q1, k1, q2, k2, v, doc_ids, row_scale, coef, b, bounds=bounds, score_norms=score_norms,
+            rope=tabs)
+        cs, sn = tabs if tabs is not None else (None, None)
+        ctx.save_for_backward(q1, k1, q2, k2, v, dstart, qend, sc, coef_f, b_f, cs, sn)
         ctx.K, ctx.degree, ctx.shared = K, degree, shared
         ctx.has_coef, ctx.has_b = coef is not None, b is not None
         ctx.coef_dtype = coef.dtype if coef is not None else None
@@ -216,13 +262,13 @@ class PolyAttention(torch.autograd.Function):
 
     @staticmethod
     def backward(ctx, do):
-        q1, k1, q2, k2, v, dstart, qend, sc, coef_f, b_f = ctx.saved_tensors
+        q1, k1, q2, k2, v, dstart, qend, sc, coef_f, b_f, cs, sn = ctx.saved_tensors
         K = ctx.K
         dq1, dk1, dq2, dk2, dv, dpar = _run_backward(K, ctx.degree, q1, k1, q2, k2, v, dstart, qend, sc, coef_f,
-                                                      b_f, do)
+                                                      b_f, do, rope=(cs, sn) if cs is not None else None)
         dcoef = dpar.to(ctx.coef_dtype) if (K == _abi.LOWER_DEGREE_MIX and ctx.has_coef) else None
         db = dpar[:, 0].to(ctx.b_dtype) if (K == _abi.OFFSET_SQUARE and ctx.has_b) else None
-        return None, dq1, dk1, dq2, dk2, dv, None, None, dcoef, db, None, None, None
+        return None, dq1, dk1, dq2, dk2, dv, None, None, dcoef, db, None, None, None, None
 
 
 def _alloc_like(x: torch.Tensor) -> torch.Tensor:
@@ -230,14 +276,17 @@ def _alloc_like(x: torch.Tensor) -> torch.Tensor:
     return y if _aligned_rows(y) else torch.empty(x.shape, dtype=x.dtype, device=x.device)
 
 
-def _problem(K, degree, q1, k1, q2, k2, v, dstart, qend, sc, coef_f, b_f, score_norms=None) -> _abi.Problem:
+def _problem(K, degree, q1, k1, q2, k2, v, dstart, qend, sc, coef_f, b_f, score_norms=None,
+             rope=None) -> _abi.Problem:
     B, H, T, DK = q1.shape
     return _abi.Problem(B, H, T, DK, v.shape[-1], K, int(degree) if degree is not None else 0, _DTYPES[q1.dtype],
                         _desc(q1), _desc(k1), _desc(q2), _desc(k2), _desc(v),
                         dstart.data_ptr(), qend.data_ptr(), sc.data_ptr(),
                         coef_f.data_ptr() if coef_f is not None else None,
                         b_f.data_ptr() if b_f is not None else None,
-                        score_norms.data_ptr() if score_norms is not None else None)
+                        score_norms.data_ptr() if score_norms is not None else None,
+                        rope[0].data_ptr() if rope is not None else None,
+                        rope[1].data_ptr() if rope is not None else None)
 
 
 def score_norm_buffer(kind, q1, k1, q2=None, k2=None) -> torch.Tensor:
@@ -255,16 +304,20 @@ def score_bound(score_norms: torch.Tensor, d_key: int) -> dict:
 
 
 def poly_attention_hip(kind, q1, k1, q2, k2, v, doc_ids, row_scale, coef=None, b=None, *, degree=None,
-                       bounds=None, score_norms=None):
+                       bounds=None, score_norms=None, rope=None):
     """q*, k*: (B, H, T, dk); v: (B, H, T, dv); doc_ids: (B, T) contiguous ids, < 0 = padding;
     row_scale: (B, T) = n_visible^-p for real queries, 0 for padding. kind="power" takes degree=p and ignores
     q2/k2. bounds: optional doc_bounds(doc_ids), computed once per batch by a caller with many layers.
     score_norms: optional zeroed float32 (pairs, 2, H) tensor (score_norm_buffer) that the forward fills with the
-    per-head max |q| and max |k| of each pair, for score_bound(). Every gradient is reduced in a fixed order
+    per-head max |q| and max |k| of each pair, for score_bound(). rope: optional (cos, sin) rotary tables
+    (rope_tables layout, ref: tnlm/attention.py:41-45): q*/k* are then the unrotated projections, rotated here in one
+    pass each exactly as the reference's apply_rope (ref: tnlm/model.py:70-71,81-82), and the backward returns their
+    gradients with the rotation's gradient applied inside the library. Every gradient is reduced in a fixed order
     (deterministic).  ref: tnlm/kernels/poly_attn.py:312-315"""
     if torch.compiler.is_compiling():
         # under torch.compile the same kernels run behind registered custom ops (opaque to the compiler)
         from .ops import poly_attention_op
         return poly_attention_op(kind, q1, k1, q2, k2, v, doc_ids, row_scale, coef, b, degree=degree, bounds=bounds,
-                                 score_norms=score_norms)
-    return PolyAttention.apply(kind, q1, k1, q2, k2, v, doc_ids, row_scale, coef, b, degree, bounds, score_norms)
+                                 score_norms=score_norms, rope=rope)
+    return PolyAttention.apply(kind, q1, k1, q2, k2, v, doc_ids, row_scale, coef, b, degree, bounds, score_norms,
+                               rope)

@@ -90,6 +90,20 @@ def doc_positions(doc: torch.Tensor) -> torch.Tensor:
     return ar - first
 
 
+def rope_tables(positions: torch.Tensor, dim: int, base: float = 10000.0):
+    """(cos, sin), each (B, 1, T, dim/2) fp32, of per-token positions (B, T): ref: tnlm/attention.py:41-45."""
+    inv = 1.0 / (base ** (torch.arange(0, dim, 2, device=positions.device, dtype=torch.float32) / dim))
+    ang = positions.float()[..., None] * inv
+    return ang.cos()[:, None], ang.sin()[:, None]
+
+
+def apply_rope(x: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor) -> torch.Tensor:
+    """The reference's unfused rotary embedding as separate tensor operations (ref: tnlm/attention.py:48-51): the
+    checker of the one-pass kernel and, through autograd, of its inverse."""
+    x1, x2 = x.to(torch.promote_types(x.dtype, torch.float32)).chunk(2, dim=-1)
+    return torch.cat([x1 * cos - x2 * sin, x1 * sin + x2 * cos], dim=-1).to(x.dtype)
+
+
 def row_scale(doc: torch.Tensor, power: float) -> torch.Tensor:
     """(pos + 1)^-power for real tokens, 0 for padding (ref: tests/test_kernels.py:30-32, tnlm/model.py:217-221)."""
     pos = doc_positions(doc)

@@ -33,7 +33,7 @@ def _declared_functions(header=HEADER):
 
 def test_library_loads_and_reports_abi_version(lib):
     from tensor_train_ing_amd import _abi
-    assert lib.tnpa_abi_version() == _abi.ABI_VERSION == 3
+    assert lib.tnpa_abi_version() == _abi.ABI_VERSION == 4
 
 
 def test_every_declared_symbol_is_exported(lib):
@@ -65,6 +65,8 @@ int main(void) {
          offsetof(tnpa_problem_t, doc_start), offsetof(tnpa_problem_t, offset));
   printf("%zu %zu %zu %zu\n", offsetof(tnpa_grads_t, dv), offsetof(tnpa_grads_t, dpar),
          offsetof(tnpa_grads_t, workspace), offsetof(tnpa_grads_t, workspace_bytes));
+  printf("%zu %zu %zu\n", offsetof(tnpa_problem_t, score_norms), offsetof(tnpa_problem_t, rope_cos),
+         offsetof(tnpa_problem_t, rope_sin));
   return 0;
 }''')
     exe = tmp_path / "layout"
@@ -76,6 +78,7 @@ int main(void) {
     assert got[0] == [ctypes.sizeof(_abi.Tensor), ctypes.sizeof(P), ctypes.sizeof(G)]
     assert got[1] == [P.q1.offset, P.v.offset, P.doc_start.offset, P.offset.offset]
     assert got[2] == [G.dv.offset, G.dpar.offset, G.workspace.offset, G.workspace_bytes.offset]
+    assert got[3] == [P.score_norms.offset, P.rope_cos.offset, P.rope_sin.offset]
 
 
 def _problem(**kw):
@@ -95,6 +98,7 @@ def _problem(**kw):
     ("kind", 7, 1, "unknown kind"),
     ("degree", 0, 1, "degree"),
     ("dtype", 9, 1, "dtype"),
+    ("rope_cos", 4096, 1, "both or neither"),
     ("doc_start", None, 1, "tnpa_doc_bounds"),
     ("row_scale", None, 1, "row_scale"),
 ])
@@ -214,6 +218,10 @@ def test_backward_plan(lib):
         "scale", "kv", "q"]
     assert _launches(lib, _problem(), _abi.X_PRESCALE_ON) == ["scale", "kv", "q"]
     assert _launches(lib, _problem(dtype=_abi.F32), _abi.X_PRESCALE_OFF) == ["kv", "q"]
+    # rotary tables: the gradient of the rotation is applied to dq / dk after the other launches
+    assert _launches(lib, _problem(rope_cos=4096, rope_sin=8192)) == ["kv", "q", "rope"]
+    assert _launches(lib, _problem(kind=_abi.OFFSET_SQUARE, offset=4096, rope_cos=4096, rope_sin=8192)) == [
+        "kv", "q", "dpar", "rope"]
     assert lib.tnpa_x_launch_name(ctypes.byref(_problem()), 0, 5) == b""
 
 
@@ -261,3 +269,17 @@ def test_product_never_imports_the_oracle():
     for f in (ROOT / "tensor_train_ing_amd").rglob("*.py"):
         src = f.read_text()
         assert not re.search(r"^\s*(from|import)\s+oracle\b", src, flags=re.M), f
+
+
+def test_rope_tables_are_checked():
+    """rope=(cos, sin): the reference's (B, 1, T, dk/2) layout or (B, T, dk/2), fp32 after conversion, no gradient."""
+    from tensor_train_ing_amd.poly_attn import rope_tables_of
+    q = torch.zeros(2, 3, 10, 16)
+    cs, sn = rope_tables_of((torch.ones(2, 1, 10, 8), torch.zeros(2, 10, 8, dtype=torch.float64)), q)
+    assert cs.shape == sn.shape == (2, 10, 8) and cs.dtype == sn.dtype == torch.float32 and sn.is_contiguous()
+    with pytest.raises(ValueError, match="expected"):
+        rope_tables_of((torch.ones(2, 10, 16), torch.ones(2, 10, 8)), q)
+    with pytest.raises(ValueError, match="pair"):
+        rope_tables_of(torch.ones(2, 10, 8), q)
+    with pytest.raises(ValueError, match="differentiable"):
+        rope_tables_of((torch.ones(2, 10, 8, requires_grad=True), torch.ones(2, 10, 8)), q)

@@ -132,3 +132,31 @@ def test_custom_op_equals_autograd_function(kind):
     assert len(outs[0]) == len(outs[1])
     for a, b_ in zip(*outs):
         assert torch.equal(a, b_)
+
+
+@pytest.mark.parametrize("kind", ["power", "signed_product"])
+def test_custom_op_with_rope_equals_autograd_function(kind):
+    """With rotary tables the custom-op path rotates through tnpa::rope (gradient: the inverse rotation op) and the
+    autograd Function applies the inverse inside the backward: the same arithmetic, bit-identical results."""
+    from poly_ref import doc_positions, gaussian_inputs, rope_tables, row_scale
+    from tensor_train_ing_amd import poly_attention_hip, poly_attention_op
+    dev = torch.device("cuda:0")
+    print(f"[custom op rope] kind={kind}", flush=True)
+    two = kind == "signed_product"
+    q1, k1, q2, k2, v, do = (x.to(dev) for x in gaussian_inputs(2, 3, 160, 128, 128, torch.bfloat16, 7,
+                                                                 qk_scale=128 ** -0.25, two_pairs=True))
+    doc = torch.zeros(2, 160, dtype=torch.long, device=dev)
+    doc[0, 50:] = 1
+    rs = row_scale(doc, 0.5)
+    rope = rope_tables(doc_positions(doc), 128)
+    outs = []
+    for fn in (poly_attention_hip, poly_attention_op):
+        ins = [x.detach().clone().requires_grad_() for x in (q1, k1, q2, k2, v)]
+        o = fn(kind, ins[0], ins[1], ins[2] if two else None, ins[3] if two else None, ins[4], doc, rs,
+               degree=2 if kind == "power" else None, rope=rope)
+        o.backward(do)
+        outs.append([o.detach()] + [t.grad for t in ins if t.grad is not None])
+    torch.cuda.synchronize()
+    assert len(outs[0]) == len(outs[1])
+    for a, b_ in zip(*outs):
+        assert torch.equal(a, b_)
