@@ -87,6 +87,29 @@ def make_inputs(B, H, T, D, boost, seed, device, two_pairs=False, doc_len=0, dty
     return q, k, v, do, doc, rs
 
 
+def rope_tables_for(doc, D, base=10000.0):
+    """Rotary tables (B, 1, T, D/2) fp32 from positions within documents, built as the reference model builds them
+    once per batch (ref: tnlm/attention.py:41-45 on doc positions, ref: tnlm/model.py:205-210): caller-side setup,
+    not part of the timed step."""
+    import torch
+    B, T = doc.shape
+    ar = torch.arange(T, device=doc.device).expand(B, T)
+    start = torch.ones_like(doc, dtype=torch.bool)
+    start[:, 1:] = doc[:, 1:] != doc[:, :-1]
+    pos = ar - torch.where(start, ar, torch.zeros_like(ar)).cummax(-1).values
+    inv = 1.0 / (base ** (torch.arange(0, D, 2, device=doc.device, dtype=torch.float32) / D))
+    ang = pos.float()[..., None] * inv
+    return ang.cos()[:, None], ang.sin()[:, None]
+
+
+def torch_apply_rope(x, cos, sin):
+    """The reference's rotation as separate tensor operations (ref: tnlm/attention.py:48-51): the unfused step that
+    --rope compares against."""
+    import torch
+    x1, x2 = x.to(torch.promote_types(x.dtype, torch.float32)).chunk(2, dim=-1)
+    return torch.cat([x1 * cos - x2 * sin, x1 * sin + x2 * cos], dim=-1).to(x.dtype)
+
+
 def event_intervals(fn, reps):
     """Runs fn reps times back to back with a HIP event between consecutive runs on the current stream; returns
     the reps intervals (ms)."""
@@ -354,6 +377,10 @@ def main(argv=None):
     ap.add_argument("--doc-len", type=int, default=0,
                     help="contiguous documents of this many tokens per row (0: one document; FLOPs count only the "
                          "visible pairs, so the rate shows how well invisible tiles are skipped)")
+    ap.add_argument("--rope", action="store_true",
+                    help="q/k enter unrotated with rotary tables (positions within documents): the step includes the "
+                         "one-pass rotation and the rotation's gradient inside the backward; also times the "
+                         "reference's way (torch apply_rope, then the operator, autograd through both)")
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--kernel-reps", type=int, default=50)
@@ -400,13 +427,20 @@ def main(argv=None):
         x.requires_grad_()
     deg = degree if kind == "power" else None
 
+    rope = rope_tables_for(doc, D) if a.rope else None
+
     def step():
-        out = poly_attention_hip(kind, q, k, q2, k2, v, doc, rs, coef=coef, b=bias, degree=deg)
+        out = poly_attention_hip(kind, q, k, q2, k2, v, doc, rs, coef=coef, b=bias, degree=deg, rope=rope)
+        return torch.autograd.grad(out, leaves, do)
+
+    def step_torch_rope():
+        rot = lambda x: None if x is None else torch_apply_rope(x, *rope)  # noqa: E731
+        out = poly_attention_hip(kind, rot(q), rot(k), rot(q2), rot(k2), v, doc, rs, coef=coef, b=bias, degree=deg)
         return torch.autograd.grad(out, leaves, do)
 
     def fwd_only():
         with torch.no_grad():
-            return poly_attention_hip(kind, q, k, q2, k2, v, doc, rs, coef=coef, b=bias, degree=deg)
+            return poly_attention_hip(kind, q, k, q2, k2, v, doc, rs, coef=coef, b=bias, degree=deg, rope=rope)
 
     for _ in range(a.warmup):
         step()
@@ -417,6 +451,19 @@ def main(argv=None):
     wall_ms = (time.perf_counter() - t0) * 1e3 / a.steps
     ms = sum(iv) / len(iv)
     fwd_iv = event_intervals(fwd_only, a.steps)
+    rope_info = None
+    if a.rope:
+        for _ in range(a.warmup):
+            step_torch_rope()
+        torch.cuda.synchronize()
+        trope = event_intervals(step_torch_rope, a.steps)
+        from tensor_train_ing_amd.poly_attn import rope_rotate, rope_tables_of
+        cs, sn = rope_tables_of(rope, q)
+        qd = q.detach()
+        rope_info = {"ms_per_step_fused": round(statistics.median(iv), 4),
+                     "ms_per_step_torch_apply_rope": round(statistics.median(trope), 4),
+                     "rope_kernel_ms_per_tensor": round(median_each(lambda: rope_rotate(qd, cs, sn), a.kernel_reps),
+                                                        4)}
 
     # counted FLOPs (exact causal pairs): one q/k pair fwd 2 matmul units of 2*B*H*Npairs*D, fwd+bwd 7; two pairs
     # fwd 3 (S1, S2, PV), fwd+bwd 11
@@ -439,8 +486,10 @@ def main(argv=None):
         "vs_baseline": None, "dtype": a.dtype, "data": "synthetic",
         "config": {"workload": f"polynomial attention fwd+bwd, BASELINE config '{a.config}': B{B} H{H} T{T} D{D} "
                                + (f"degree {degree}" if kind == "power" else f"kind {kind}")
-                               + f", causal{docs}, row scale (position in document + 1)^-1/2",
-                   "B": B, "H": H, "T": T, "D": D, "kind": kind, "degree": deg, "doc_len": a.doc_len or T},
+                               + f", causal{docs}, row scale (position in document + 1)^-1/2"
+                               + (", rotary embedding of q/k inside the operator" if a.rope else ""),
+                   "B": B, "H": H, "T": T, "D": D, "kind": kind, "degree": deg, "doc_len": a.doc_len or T,
+                   "rope": a.rope},
         "pct_of_peak": round(100 * value / peak, 2),
         "ms_per_step_median": round(statistics.median(iv), 4),
         "fwd_ms_median": round(fwd_med, 4),
@@ -453,7 +502,9 @@ def main(argv=None):
                      "traffic": (measured_traffic(a.config, dom)
                                  if kind == "power" and not a.doc_len and a.dtype == "bf16" else None)},
     }
-    if not a.no_cpu_baseline and kind == "power" and not a.doc_len:
+    if rope_info is not None:
+        line["rope"] = rope_info
+    if not a.no_cpu_baseline and kind == "power" and not a.doc_len and not a.rope:
         line["cpu_baseline"] = cpu_baseline(q, k, v, do, rs, degree, a.cpu_seconds)
     print(json.dumps(line), flush=True)
     return 0

@@ -453,7 +453,7 @@ constexpr int64_t kMaxDsTileBytes = 4LL << 30;
 struct Plan {
   int n = 0;
   int what[7] = {0, 0, 0, 0, 0, 0, 0};
-  bool prescale = false, par = false, ds = false;
+  bool prescale = false, par = false, ds = false, rope_in_epilogue = false;
   int nnb = 0;  // key blocks per row (dpar partials)
   int64_t dpar_off = 0, dos_off = 0, ds_off = 0, ds2_off = 0, bytes = 0;
 };
@@ -495,7 +495,9 @@ int make_plan(const tnpa_problem_t& p, int opts, Plan& pl) {
   }
   pl.what[pl.n++] = pl.ds ? L_QDS : L_Q;
   if (pl.par) pl.what[pl.n++] = L_DPAR;
-  if (p.rope_cos != nullptr) pl.what[pl.n++] = L_ROPE;
+  // the rotary tables' gradient: in the dQ / dK epilogues where they write whole rows, else one pass at the end
+  pl.rope_in_epilogue = p.rope_cos != nullptr && tnpa::rope_epilogue(f32, poly, dk, dv);
+  if (p.rope_cos != nullptr && !pl.rope_in_epilogue) pl.what[pl.n++] = L_ROPE;
   return TNPA_OK;
 }
 
@@ -537,6 +539,10 @@ int run_backward(const tnpa_problem_t* problem, const tnpa_grads_t* grads, int o
     dos = tnpa_tensor_t{ws + pl.dos_off, (int64_t)p.heads * p.seq_len * st, (int64_t)p.seq_len * st, st};
     k.dsc = desc(dos);
     k.dpre = 1;
+  }
+  if (pl.rope_in_epilogue) {
+    k.rcos = p.rope_cos;
+    k.rsin = p.rope_sin;
   }
   if (pl.ds) {
     k.dstile = ws + pl.ds_off;

@@ -231,6 +231,58 @@ template <typename T, int ROWS, int D, int WID, int NT> struct Stage {
       }
     }
   }
+  // copy_out with the gradient of a rotary embedding applied to every row (ref: tnlm/attention.py:48-51 and its
+  // autograd): row rr is token row0 + rr, whose tables start at cs / sn + (trow0 + rr) * D/2. Chunk c of a row pairs
+  // with chunk c ^ NCHG/2 (columns j and j + D/2), held by thread idx ^ NCHG/2 = lane ^ NCHG/2 of the same wave;
+  // out = (g1 cos + g2 sin, g2 cos - g1 sin) in fp32, each product and sum rounded on its own, then rounded to T.
+  // The table loads of RG chunks are issued together before any of them is used (one memory latency per group).
+  __device__ inline void copy_out_rope(const char TNPA_LDS* tile, T* __restrict__ g, int64_t st, int row0, int nvalid,
+                                       const float* __restrict__ cs, const float* __restrict__ sn, int64_t trow0) const {
+#pragma clang fp contract(off)
+    static_assert(NT % NCHG == 0 && NCHG >= 2 && NCHG / 2 <= 32, "row chunks within one wave");
+    typedef float f32x4_ __attribute__((ext_vector_type(4)));
+    constexpr int HC = NCHG / 2, HALF = D / 2, NV = CE / 4, RG = PER < 4 ? PER : 4;
+#pragma unroll
+    for (int i0 = 0; i0 < PER; i0 += RG) {
+      f32x4_ cv[RG][NV], sv[RG][NV];
+      u32x4 own[RG], oth[RG];
+#pragma unroll
+      for (int u = 0; u < RG; ++u) {
+        const int idx = (int)threadIdx.x + (i0 + u) * NT;
+        const int rr = idx / NCHG, c = idx % NCHG;
+        const bool ok = (TOTAL % NT == 0 || idx < TOTAL) && rr < nvalid;
+        const int64_t to = (trow0 + (ok ? rr : 0)) * HALF + (c % HC) * CE;
+#pragma unroll
+        for (int v = 0; v < NV; ++v) {
+          cv[u][v] = *(const f32x4_*)(cs + to + 4 * v);
+          sv[u][v] = *(const f32x4_*)(sn + to + 4 * v);
+        }
+        own[u] = u32x4{0u, 0u, 0u, 0u};
+        if (TOTAL % NT == 0 || idx < TOTAL) own[u] = *(const u32x4 TNPA_LDS*)(tile + TL::off(rr, c * CE));
+#pragma unroll
+        for (int e = 0; e < 4; ++e) oth[u][e] = (uint32_t)__shfl_xor((int)own[u][e], HC, 64);
+      }
+#pragma unroll
+      for (int u = 0; u < RG; ++u) {
+        const int idx = (int)threadIdx.x + (i0 + u) * NT;
+        const int rr = idx / NCHG, c = idx % NCHG;
+        if ((TOTAL % NT == 0 || idx < TOTAL) && rr < nvalid) {
+          const bool lo = c < HC;
+          u32x4 a = lo ? own[u] : oth[u], b = lo ? oth[u] : own[u], res;
+          const T* e1 = reinterpret_cast<const T*>(&a);
+          const T* e2 = reinterpret_cast<const T*>(&b);
+          T* eo = reinterpret_cast<T*>(&res);
+#pragma unroll
+          for (int j = 0; j < CE; ++j) {
+            const float g1 = (float)e1[j], g2 = (float)e2[j], c1 = cv[u][j / 4][j % 4], s1 = sv[u][j / 4][j % 4];
+            const float p1 = g1 * c1, p2 = g2 * s1, p3 = g1 * s1, p4 = g2 * c1;
+            eo[j] = (T)(lo ? p1 + p2 : p4 - p3);
+          }
+          *(u32x4*)(g + (int64_t)(row0 + rr) * st + c * CE) = res;
+        }
+      }
+    }
+  }
   // Chunk i through a buffer resource over the tile's rows (rows past the resource's end read as zero): one
   // instruction, no address arithmetic or branch, so it can sit between matrix instructions. voff = byte offset of
   // the thread's chunk i inside the tile. Needs TOTAL % NT == 0.

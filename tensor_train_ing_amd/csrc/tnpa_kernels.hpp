@@ -655,6 +655,7 @@ k_bwd_q(const KParams p) {
   typedef Tile<T, BM, DKP> QTile;
   typedef Tile<T, BM, DVP> DOTile;
   constexpr bool ROWLDS = DKP == DK && DVP == DV && NPAIR * QTile::BYTES + DOTile::BYTES <= LDS_CAP;
+  static_assert(!rope_epilogue_cfg<T, POLY, DK, DV>() || ROWLDS, "rotary gradient in the dQ epilogue needs row output");
   constexpr int SMEM = cmax(NBUF * BUF, cmax(ROWLDS ? NPAIR * QTile::BYTES + DOTile::BYTES : 0, QTile::BYTES));
   static_assert(SMEM <= LDS_CAP, "LDS");
   __shared__ __attribute__((aligned(16))) char smem_[SMEM];
@@ -914,7 +915,11 @@ k_bwd_q(const KParams p) {
       acc_rows_to_lds<T, QTile, NDK>(smem, 32 * (wave * QW + s), l32, h, dq[pr][s], p.gf, DK);
     __syncthreads();
     Stage<T, BM, DK, DKP, NT> os;
-    os.copy_out(smem, head_ptr_w<T>(*outs[pr], b, hd), outs[pr]->st, m0, T_ - m0);
+    if (p.rcos != nullptr)
+      os.copy_out_rope(smem, head_ptr_w<T>(*outs[pr], b, hd), outs[pr]->st, m0, T_ - m0, p.rcos, p.rsin,
+                       (int64_t)b * T_ + m0);
+    else
+      os.copy_out(smem, head_ptr_w<T>(*outs[pr], b, hd), outs[pr]->st, m0, T_ - m0);
   }
 }
 
@@ -952,6 +957,7 @@ k_bwd_kv(const KParams p) {
   typedef Tile<T, BNK, DKP> KRows;
   typedef Tile<T, BNK, DVP> VRows;
   constexpr bool ROWLDS = DKP == DK && DVP == DV && NPAIR == 1 && KRows::BYTES + VRows::BYTES <= 160 * 1024 - 16 * NW;
+  static_assert(!rope_epilogue_cfg<T, POLY, DK, DV>() || ROWLDS, "rotary gradient in the dK epilogue needs row output");
   constexpr int SMEM = cmax(NBUF * BUF, cmax(ROWLDS ? NPAIR * KRows::BYTES + VRows::BYTES : 0, cmax(KRows::BYTES, VRows::BYTES)));
   static_assert(SMEM <= 160 * 1024 - 16 * NW, "LDS");
   __shared__ __attribute__((aligned(16))) char smem_[SMEM];
@@ -1312,7 +1318,11 @@ k_bwd_kv(const KParams p) {
         for (int s = 0; s < KW; ++s) acc_rows_to_lds<T, KRows, NDK>(smem, 32 * (wave * KW + s), l32, h, dk[pr][s], p.gf, DK);
         __syncthreads();
         Stage<T, BNK, DK, DKP, NT> os;
-        os.copy_out(smem, head_ptr_w<T>(*kouts[pr], b, hd), kouts[pr]->st, n0, T_ - n0);
+        if (p.rcos != nullptr)
+          os.copy_out_rope(smem, head_ptr_w<T>(*kouts[pr], b, hd), kouts[pr]->st, n0, T_ - n0, p.rcos, p.rsin,
+                           (int64_t)b * T_ + n0);
+        else
+          os.copy_out(smem, head_ptr_w<T>(*kouts[pr], b, hd), kouts[pr]->st, n0, T_ - n0);
       }
     }
   } else {
@@ -1543,7 +1553,10 @@ k_bwd_kv_pair(const KParams p) {
     __syncthreads();
     {
       Stage<T, BNK, DK, DK, 512> os;
-      os.copy_out(smem, head_ptr_w<T>(p.dk1, b, hd), p.dk1.st, n0, T_ - n0);
+      if (p.rcos != nullptr)
+        os.copy_out_rope(smem, head_ptr_w<T>(p.dk1, b, hd), p.dk1.st, n0, T_ - n0, p.rcos, p.rsin, (int64_t)b * T_ + n0);
+      else
+        os.copy_out(smem, head_ptr_w<T>(p.dk1, b, hd), p.dk1.st, n0, T_ - n0);
     }
   } else {
     __syncthreads();  // the producers have their K / V operands: the row area is free
@@ -1647,7 +1660,10 @@ k_bwd_kv_pair(const KParams p) {
     __syncthreads();
     {
       Stage<T, BNK, DK, DK, 512> os;
-      os.copy_out(smem, head_ptr_w<T>(p.dk1, b, hd), p.dk1.st, n0, T_ - n0);
+      if (p.rcos != nullptr)
+        os.copy_out_rope(smem, head_ptr_w<T>(p.dk1, b, hd), p.dk1.st, n0, T_ - n0, p.rcos, p.rsin, (int64_t)b * T_ + n0);
+      else
+        os.copy_out(smem, head_ptr_w<T>(p.dk1, b, hd), p.dk1.st, n0, T_ - n0);
     }
   }
 
@@ -1817,7 +1833,10 @@ k_bwd_q_ds(const KParams p) {
   acc_rows_to_lds<T, QTile, NDK>(smem, 32 * wave, l32, h, dq, p.gf, DK);
   __syncthreads();
   Stage<T, BM, DK, DK, NT> os;
-  os.copy_out(smem, head_ptr_w<T>(p.dq1, b, hd), p.dq1.st, m0, T_ - m0);
+  if (p.rcos != nullptr)
+    os.copy_out_rope(smem, head_ptr_w<T>(p.dq1, b, hd), p.dq1.st, m0, T_ - m0, p.rcos, p.rsin, (int64_t)b * T_ + m0);
+  else
+    os.copy_out(smem, head_ptr_w<T>(p.dq1, b, hd), p.dq1.st, m0, T_ - m0);
 }
 
 // ------------------------------------------------------------------------------------------------ launchers

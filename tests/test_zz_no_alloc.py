@@ -16,7 +16,7 @@ from poly_ref import gaussian_inputs, rel_fro, row_scale
 pytestmark = pytest.mark.gpu
 
 
-def _run(entry, kind, B, H, T, D, seed):
+def _run(entry, kind, B, H, T, D, seed, rope=False):
     from tensor_train_ing_amd import _abi
     from tensor_train_ing_amd.poly_attn import KINDS, _desc, _problem, _stream, doc_bounds
     lib = _abi.load()
@@ -30,8 +30,13 @@ def _run(entry, kind, B, H, T, D, seed):
     rs = row_scale(doc, 0.5).float().contiguous()
     coef = torch.tensor([[0.3, -0.5, 0.7, 1.1]], device="cuda").repeat(H, 1).contiguous()
     bb = torch.linspace(-1, 1.5, H, device="cuda").contiguous()
+    tabs = None
+    if rope:  # q/k stand for rotated inputs; the backward applies the rotation's gradient to dq / dk
+        from poly_ref import doc_positions, rope_tables
+        cos, sin = rope_tables(doc_positions(doc), D)
+        tabs = (cos[:, 0].contiguous(), sin[:, 0].contiguous())
     prob = _problem(KINDS[kind], 2, q1, k1, q2 if two else q1, k2 if two else k1, v, dstart, qend, rs,
-                    coef if kind == "lower_degree_mix" else None, bb if kind == "offset_square" else None)
+                    coef if kind == "lower_degree_mix" else None, bb if kind == "offset_square" else None, rope=tabs)
     out = {n: torch.full_like(x, float("nan")) for n, x in (("dq1", q1), ("dk1", k1), ("dv", v), ("dq2", q1),
                                                               ("dk2", k1))}
     out["dpar"] = torch.full((H, 4), float("nan"), device="cuda")
@@ -47,13 +52,14 @@ def _run(entry, kind, B, H, T, D, seed):
     return {n: out[n] for n in keep}
 
 
-@pytest.mark.parametrize("kind,D", [("offset_square", 64), ("lower_degree_mix", 64), ("offset_square", 128),
-                                    ("power", 128)])
-def test_noalloc_backward_equals_workspace_backward(kind, D):
-    print(f"[noalloc] kind={kind} D={D}", flush=True)
+@pytest.mark.parametrize("kind,D,rope", [("offset_square", 64, False), ("lower_degree_mix", 64, False),
+                                         ("offset_square", 128, False), ("power", 128, False), ("power", 128, True),
+                                         ("signed_product", 64, True)])
+def test_noalloc_backward_equals_workspace_backward(kind, D, rope):
+    print(f"[noalloc] kind={kind} D={D} rope={rope}", flush=True)
     for B, H, T, seed in ((2, 4, 700, 1), (1, 2, 190, 2)):  # the second call is smaller
-        a = _run("tnpa_backward", kind, B, H, T, D, seed)
-        b = _run("tnpa_backward_noalloc", kind, B, H, T, D, seed)
+        a = _run("tnpa_backward", kind, B, H, T, D, seed, rope)
+        b = _run("tnpa_backward_noalloc", kind, B, H, T, D, seed, rope)
         for n in a:
             assert torch.isfinite(a[n]).all(), n
             if n == "dq1" and D == 128 and kind in ("power", "offset_square"):
