@@ -36,10 +36,15 @@ def fast_context(doc_ids: torch.Tensor, positions: torch.Tensor, powers, backend
             "bounds": doc_bounds(doc_ids)}
 
 
-def attention(kind: str, q1, k1, q2, k2, v, ctx: dict, row_power: float, coef=None, b=None, degree=None):
-    """Attention.forward's fast-path call (ref: tnlm/model.py:86-91) for ctx["backend"] == "hip": (B, H, T, dv)."""
+def attention(kind: str, q1, k1, q2, k2, v, ctx: dict, row_power: float, coef=None, b=None, degree=None,
+              rope=None):
+    """Attention.forward's fast-path call (ref: tnlm/model.py:86-91) for ctx["backend"] == "hip": (B, H, T, dv).
+    rope: ctx["rope"] when q/k are the unrotated projections (ref: tnlm/model.py:69-71,81-82 then run inside the
+    operator), None when the caller has rotated them."""
     fn = poly_attention_for(ctx["backend"])
     kw = {"degree": degree} if kind == "power" else {}
+    if rope is not None:
+        kw["rope"] = rope
     return fn(kind, q1, k1, q2, k2, v, ctx["doc_ids"], ctx["row_scale"][row_power], coef=coef, b=b,
               bounds=ctx.get("bounds"), **kw)
 

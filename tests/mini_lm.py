@@ -73,19 +73,21 @@ class Block(nn.Module):
 
     def attention(self, x, ctx):
         cos, sin = ctx["rope"]
-        q1 = rope(self._heads(x, self.q1, self.dk), cos, sin)
-        k1 = rope(self._heads(x, self.k1, self.dk), cos, sin)
+        fused = ctx["backend"] != "reference"  # the HIP operator rotates q/k itself (rope=)
+        rot = (lambda t: t) if fused else (lambda t: rope(t, cos, sin))  # noqa: E731
+        q1 = rot(self._heads(x, self.q1, self.dk))
+        k1 = rot(self._heads(x, self.k1, self.dk))
         q2 = k2 = None
         if self.kind in TWO_PAIRS:
-            q2 = rope(self._heads(x, self.q2, self.dk), cos, sin)
-            k2 = rope(self._heads(x, self.k2, self.dk), cos, sin)
+            q2 = rot(self._heads(x, self.q2, self.dk))
+            k2 = rot(self._heads(x, self.k2, self.dk))
         v = self._heads(x, self.v, self.dv)
         coef, b = getattr(self, "coef", None), getattr(self, "b", None)
         if ctx["backend"] == "reference":
             y = dense_attention(self.kind, q1, k1, q2, k2, v, ctx["C"][self.row_power], coef, b, self.degree)
         else:
             y = model_glue.attention(self.kind, q1, k1, q2, k2, v, ctx, self.row_power, coef=coef, b=b,
-                                     degree=self.degree if self.kind == "power" else None)
+                                     degree=self.degree if self.kind == "power" else None, rope=ctx["rope"])
         B, H, T, dv = y.shape
         return self.o(y.transpose(1, 2).reshape(B, T, H * dv))
 
