@@ -453,7 +453,7 @@ constexpr int64_t kMaxDsTileBytes = 4LL << 30;
 struct Plan {
   int n = 0;
   int what[7] = {0, 0, 0, 0, 0, 0, 0};
-  bool prescale = false, par = false, ds = false, rope_in_epilogue = false;
+  bool prescale = false, par = false, ds = false;
   int nnb = 0;  // key blocks per row (dpar partials)
   int64_t dpar_off = 0, dos_off = 0, ds_off = 0, ds2_off = 0, bytes = 0;
 };
@@ -495,9 +495,9 @@ int make_plan(const tnpa_problem_t& p, int opts, Plan& pl) {
   }
   pl.what[pl.n++] = pl.ds ? L_QDS : L_Q;
   if (pl.par) pl.what[pl.n++] = L_DPAR;
-  // the rotary tables' gradient: in the dQ / dK epilogues where they write whole rows, else one pass at the end
-  pl.rope_in_epilogue = p.rope_cos != nullptr && tnpa::rope_epilogue(f32, poly, dk, dv);
-  if (p.rope_cos != nullptr && !pl.rope_in_epilogue) pl.what[pl.n++] = L_ROPE;
+  // rotary tables: the dQ epilogues and (one pair, head dims >= 32) the dK epilogue apply the rotation's gradient;
+  // otherwise dK gets it in one pass at the end
+  if (p.rope_cos != nullptr && !tnpa::rope_dk_epilogue(f32, poly, dk, dv)) pl.what[pl.n++] = L_ROPE;
   return TNPA_OK;
 }
 
@@ -540,10 +540,10 @@ int run_backward(const tnpa_problem_t* problem, const tnpa_grads_t* grads, int o
     k.dsc = desc(dos);
     k.dpre = 1;
   }
-  if (pl.rope_in_epilogue) {
-    k.rcos = p.rope_cos;
-    k.rsin = p.rope_sin;
-  }
+  // rotary tables: the dQ / dK epilogues apply the rotation's gradient (dK only where rope_dk_epilogue holds;
+  // the other key-side kernels never read the tables)
+  k.rcos = p.rope_cos;
+  k.rsin = p.rope_sin;
   if (pl.ds) {
     k.dstile = ws + pl.ds_off;
     if (two_pairs(p.kind)) k.dstile2 = ws + pl.ds2_off;
@@ -575,10 +575,7 @@ int run_backward(const tnpa_problem_t* problem, const tnpa_grads_t* grads, int o
         break;
       }
       case L_ROPE:
-        // the gradient of the caller's rotation, in place on dq and dk
-        e = rope_any<true>(p, grads->dq1, grads->dq1, stream);
-        if (e == hipSuccess) e = rope_any<true>(p, grads->dk1, grads->dk1, stream);
-        if (two_pairs(p.kind) && e == hipSuccess) e = rope_any<true>(p, grads->dq2, grads->dq2, stream);
+        e = rope_any<true>(p, grads->dk1, grads->dk1, stream);
         if (two_pairs(p.kind) && e == hipSuccess) e = rope_any<true>(p, grads->dk2, grads->dk2, stream);
         break;
       case L_DPAR: {

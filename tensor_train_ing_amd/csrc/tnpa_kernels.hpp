@@ -655,7 +655,6 @@ k_bwd_q(const KParams p) {
   typedef Tile<T, BM, DKP> QTile;
   typedef Tile<T, BM, DVP> DOTile;
   constexpr bool ROWLDS = DKP == DK && DVP == DV && NPAIR * QTile::BYTES + DOTile::BYTES <= LDS_CAP;
-  static_assert(!rope_epilogue_cfg<T, POLY, DK, DV>() || ROWLDS, "rotary gradient in the dQ epilogue needs row output");
   constexpr int SMEM = cmax(NBUF * BUF, cmax(ROWLDS ? NPAIR * QTile::BYTES + DOTile::BYTES : 0, QTile::BYTES));
   static_assert(SMEM <= LDS_CAP, "LDS");
   __shared__ __attribute__((aligned(16))) char smem_[SMEM];
@@ -957,7 +956,7 @@ k_bwd_kv(const KParams p) {
   typedef Tile<T, BNK, DKP> KRows;
   typedef Tile<T, BNK, DVP> VRows;
   constexpr bool ROWLDS = DKP == DK && DVP == DV && NPAIR == 1 && KRows::BYTES + VRows::BYTES <= 160 * 1024 - 16 * NW;
-  static_assert(!rope_epilogue_cfg<T, POLY, DK, DV>() || ROWLDS, "rotary gradient in the dK epilogue needs row output");
+  static_assert(!rope_dk_epilogue(sizeof(T) == 4, POLY, DK, DV) || ROWLDS, "rotary gradient in the dK epilogue");
   constexpr int SMEM = cmax(NBUF * BUF, cmax(ROWLDS ? NPAIR * KRows::BYTES + VRows::BYTES : 0, cmax(KRows::BYTES, VRows::BYTES)));
   static_assert(SMEM <= 160 * 1024 - 16 * NW, "LDS");
   __shared__ __attribute__((aligned(16))) char smem_[SMEM];
@@ -1299,7 +1298,9 @@ k_bwd_kv(const KParams p) {
   for (; j < j1; ++j) step(qlo + j * BMQ, std::true_type{});
   for (; j < ntile; ++j) step(qlo + j * BMQ, std::false_type{});
 
-  // dV and dK rows: scaled in registers, then (ROWLDS) gathered in LDS and written as whole rows
+  // dV and dK rows: scaled in registers, then (ROWLDS) gathered in LDS and written as whole rows, else stored from
+  // the accumulators (the two-pair and padded-head-dim kernels: gathering in LDS there costs spills in the loop; with
+  // rotary tables their dK is rotated by a pass after the kernel)
   const TDesc* kouts[2] = {&p.dk1, &p.dk2};
   if constexpr (ROWLDS) {
     if constexpr (WANT_DV) {

@@ -34,6 +34,7 @@ struct KParams {
   void* dstile;        // dS tiles written by the key side and read by the dQ-from-dS kernel, or null (see ds_tile_*)
   void* dstile2;       // the same for the second q/k pair (dS2), or null
   const float* rcos;   // (B, T, dk/2) rotary tables: the dQ / dK epilogues apply the rotation's gradient, or null
+                       // (dQ always; dK where rope_dk_epilogue, else a pass after the key side)
   const float* rsin;
   int dpre;            // 1: dsc holds the row-scaled dout; 0: the dK/dV pass scales dout while staging it
   int kvsel;           // key-side kernels to launch: 1 = dV pass, 2 = dK pass, 3 = both (or the combined kernel)
@@ -59,14 +60,11 @@ template <typename T, int POLY, int DK, int DV> constexpr bool kv_pair_cfg() {
   return kv_pair(sizeof(T) == 4, POLY, DK, DV);
 }
 
-// Whether every kernel that writes dQ or dK for this configuration writes them through LDS as whole rows, where
-// the epilogue applies the gradient of a rotary embedding (copy_out_rope): one q/k pair and no zero-padded head
-// dims. Otherwise the backward rotates dQ / dK in a separate pass. The kernels static_assert this.
-constexpr bool rope_epilogue(bool f32, int poly, int dk, int dv) {
+// Whether the key side writes dK as whole rows from LDS, where its epilogue applies the gradient of a rotary
+// embedding (copy_out_rope): one q/k pair and no padded head dim. The two-pair and head-dim-16 key sides store dK
+// from the accumulators, and the backward rotates it in a pass after them. (Every dQ kernel writes whole rows.)
+constexpr bool rope_dk_epilogue(bool f32, int poly, int dk, int dv) {
   return !two_pair_poly(poly) && dk >= 32 && dv >= 32;
-}
-template <typename T, int POLY, int DK, int DV> constexpr bool rope_epilogue_cfg() {
-  return rope_epilogue(sizeof(T) == 4, POLY, DK, DV);
 }
 
 // Keys per dK/dV workgroup (sizes the dcoef/db partials); mirrors Cfg::KV_KEYS: eight waves of 32 keys for the split

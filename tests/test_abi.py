@@ -218,14 +218,13 @@ def test_backward_plan(lib):
         "scale", "kv", "q"]
     assert _launches(lib, _problem(), _abi.X_PRESCALE_ON) == ["scale", "kv", "q"]
     assert _launches(lib, _problem(dtype=_abi.F32), _abi.X_PRESCALE_OFF) == ["kv", "q"]
-    # rotary tables: the gradient of the rotation goes into the dQ / dK epilogues (one q/k pair, head dims >= 32),
-    # else one pass over dq / dk after the other launches
-    assert _launches(lib, _problem(rope_cos=4096, rope_sin=8192)) == ["kv", "q"]
-    assert _launches(lib, _problem(head_dim_k=128, head_dim_v=128, rope_cos=4096, rope_sin=8192)) == ["kv", "qds"]
-    assert _launches(lib, _problem(head_dim_k=16, head_dim_v=16, rope_cos=4096, rope_sin=8192)) == [
-        "scale", "kv", "q", "rope"]
-    assert _launches(lib, _problem(kind=_abi.LOWER_DEGREE_MIX, coef=4096, rope_cos=4096, rope_sin=8192)) == [
-        "scale", "kv", "q", "dpar", "rope"]
+    # rotary tables: the rotation's gradient goes into the dQ epilogues and, for one q/k pair with head dims >= 32,
+    # the dK epilogue; otherwise dK gets it in one pass at the end
+    for kw in ({}, dict(head_dim_k=128, head_dim_v=128), dict(dtype=_abi.F32, head_dim_k=32, head_dim_v=64)):
+        assert _launches(lib, _problem(rope_cos=4096, rope_sin=8192, **kw)) == _launches(lib, _problem(**kw))
+    for kw in (dict(head_dim_k=16, head_dim_v=16), dict(kind=_abi.LOWER_DEGREE_MIX, coef=4096),
+               dict(kind=_abi.SIGNED_PRODUCT, head_dim_k=128, head_dim_v=128)):
+        assert _launches(lib, _problem(rope_cos=4096, rope_sin=8192, **kw)) == _launches(lib, _problem(**kw)) + ["rope"]
     assert lib.tnpa_x_launch_name(ctypes.byref(_problem()), 0, 5) == b""
 
 
