@@ -39,6 +39,12 @@ int tnce_forward_chunk(const void* logits, int32_t dtype, int64_t n, int64_t V, 
 int tnce_backward_chunk(void* logits, int32_t dtype, int64_t n, int64_t V, int64_t ld, const int64_t* targets,
                         int64_t ignore_index, const void* lse, const void* g, void* stream);
 
+/* dW accumulation of one chunk: acc[i] += (acc type) part[i] for n elements, part in dtype (the chunk's dW matmul
+ * output, rounded as the reference's matmul output is), acc in the accumulation type; one pass instead of an
+ * upcast copy and an add. Both pointers 16-byte aligned. Replaces ref: tnlm/kernels/fused_ce.py:50
+ * (dw += (p.T @ x).to(acc)). */
+int tnce_accumulate(void* acc, const void* part, int32_t dtype, int64_t n, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -12,6 +12,7 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <algorithm>
 #include <cmath>
 
 #include "../../include/tnce.h"
@@ -173,6 +174,27 @@ __global__ void __launch_bounds__(NT) k_ce_bwd(T* __restrict__ logits, int64_t V
   for (int64_t j = head + nvec * CE + threadIdx.x; j < V; j += NT) row[j] = val(j, (A)row[j]);
 }
 
+// acc[i] += (A)part[i] over n elements: one chunk's dW product (rounded to the matmul's type, as the reference's
+// `dw += (p.T @ x).to(acc)` rounds it) added to the accumulation-type dW in one pass, 16 bytes of part per thread
+// step (grid-stride); the same single addition per element as the reference.
+template <typename T>
+__global__ void __launch_bounds__(NT) k_ce_acc(typename AccOf<T>::type* __restrict__ acc, const T* __restrict__ part,
+                                               int64_t n) {
+  typedef typename AccOf<T>::type A;
+  constexpr int CE = 16 / (int)sizeof(T);
+  const int64_t nvec = n / CE;
+  typedef unsigned int u4 __attribute__((ext_vector_type(4)));
+  const int64_t stride = (int64_t)gridDim.x * NT;
+  for (int64_t v = (int64_t)blockIdx.x * NT + threadIdx.x; v < nvec; v += stride) {
+    const u4 raw = *(const u4*)(part + v * CE);
+    const T* e = reinterpret_cast<const T*>(&raw);
+    A* d = acc + v * CE;
+#pragma unroll
+    for (int k = 0; k < CE; ++k) d[k] += (A)e[k];
+  }
+  for (int64_t j = nvec * CE + (int64_t)blockIdx.x * NT + threadIdx.x; j < n; j += stride) acc[j] += (A)part[j];
+}
+
 int check_args(const void* logits, int32_t dtype, int64_t n, int64_t V, int64_t ld, const int64_t* targets,
                const void* lse, const char* what) {
   if (dtype < TNCE_BF16 || dtype > TNCE_F64) return tnpa::set_error(TNPA_ERR_INVALID, "%s: unknown dtype %d", what, dtype);
@@ -206,9 +228,35 @@ hipError_t launch_bwd(void* logits, int64_t n, int64_t V, int64_t ld, const int6
   return hipGetLastError();
 }
 
+template <typename T> hipError_t launch_acc(void* acc, const void* part, int64_t n, hipStream_t s) {
+  typedef typename AccOf<T>::type A;
+  constexpr int CE = 16 / (int)sizeof(T);
+  const int64_t blocks = std::min<int64_t>((n / CE + NT - 1) / NT + 1, 8192);
+  if (n > 0) hipLaunchKernelGGL(k_ce_acc<T>, dim3((unsigned)blocks), dim3(NT), 0, s, (A*)acc, (const T*)part, n);
+  return hipGetLastError();
+}
+
 }  // namespace
 
 extern "C" {
+
+int tnce_accumulate(void* acc, const void* part, int32_t dtype, int64_t n, void* stream) {
+  if (dtype < TNCE_BF16 || dtype > TNCE_F64) return tnpa::set_error(TNPA_ERR_INVALID, "tnce_accumulate: unknown dtype %d", dtype);
+  if (n < 0) return tnpa::set_error(TNPA_ERR_INVALID, "tnce_accumulate: negative size");
+  if (n > 0 && (acc == nullptr || part == nullptr)) return tnpa::set_error(TNPA_ERR_INVALID, "tnce_accumulate: null pointer");
+  if (n > 0 && (((uintptr_t)acc) % 16 != 0 || ((uintptr_t)part) % 16 != 0))
+    return tnpa::set_error(TNPA_ERR_INVALID, "tnce_accumulate: pointers must be 16-byte aligned");
+  hipStream_t s = (hipStream_t)stream;
+  hipError_t e;
+  switch (dtype) {
+    case TNCE_BF16: e = launch_acc<__bf16>(acc, part, n, s); break;
+    case TNCE_F16: e = launch_acc<_Float16>(acc, part, n, s); break;
+    case TNCE_F32: e = launch_acc<float>(acc, part, n, s); break;
+    default: e = launch_acc<double>(acc, part, n, s); break;
+  }
+  if (e != hipSuccess) return tnpa::set_error(TNPA_ERR_LAUNCH, "tnce_accumulate: %s", hipGetErrorString(e));
+  return tnpa::clear_error();
+}
 
 int tnce_forward_chunk(const void* logits, int32_t dtype, int64_t n, int64_t V, int64_t ld, const int64_t* targets,
                        int64_t ignore_index, void* lse, void* row_loss, void* total, void* stream) {

@@ -92,6 +92,7 @@ class LinearCrossEntropy(torch.autograd.Function):
         gd = g.detach().to(device=x.device, dtype=acc).reshape(1).contiguous()
         rows = min(chunk, N)
         logits = torch.empty(rows, V, device=x.device, dtype=cdtype)
+        part = torch.empty(w.shape, device=x.device, dtype=cdtype)  # one chunk's dW product, reused
         lib = _abi.load()
         code = _DTYPES[cdtype]
         with torch.cuda.device(x.device):
@@ -102,8 +103,14 @@ class LinearCrossEntropy(torch.autograd.Function):
                 torch.matmul(xc[s:s + n], wc.t(), out=p)
                 _abi.check(lib.tnce_backward_chunk(_ptr(p), code, n, V, V, _ptr(tg[s:s + n]), IGNORE_INDEX,
                                                    _ptr(lse[s:s + n]), _ptr(gd), st), "linear cross-entropy backward")
-                dx[s:s + n] = (p @ wc).to(x.dtype)
-                dw += (p.t() @ xc[s:s + n]).to(acc)
+                if x.dtype == cdtype:
+                    torch.matmul(p, wc, out=dx[s:s + n])
+                else:
+                    dx[s:s + n] = (p @ wc).to(x.dtype)
+                # dw += (p^T x).to(acc): the product in cdtype, then one HIP pass adds it to the fp32/fp64 dW
+                torch.matmul(p.t(), xc[s:s + n], out=part)
+                _abi.check(lib.tnce_accumulate(_ptr(dw), _ptr(part), code, part.numel(), st),
+                           "linear cross-entropy dW")
         return dx, dw.to(w.dtype), None, None, None
 
 

@@ -165,3 +165,27 @@ def test_pilot_1b_chunk_against_torch_float32():
     assert abs(total.item() - ref.item()) <= 1e-4 * abs(ref.item())
     assert ((gx.float() - rgx.float()).abs().max() / rgx.float().abs().max()).item() <= 1e-2
     assert ((gw.float() - rgw).abs().max() / rgw.abs().max()).item() <= 1e-2
+
+
+@pytest.mark.parametrize("dtype,n", [(torch.bfloat16, 1 << 20), (torch.float16, 999), (torch.float32, 12345),
+                                     (torch.float64, 77)])
+def test_dw_accumulate_matches_reference_upcast_add(dtype, n):
+    """tnce_accumulate(acc, part) against the reference's `dw += part.to(acc)`: bit-identical (one addition per
+    element in the accumulation type), twice in a row, with a length that is not a multiple of the 16-byte step."""
+    import ctypes
+    from tensor_train_ing_amd import _abi
+    from tensor_train_ing_amd.fused_ce import _DTYPES
+    dev = torch.device("cuda:0")
+    g = torch.Generator().manual_seed(5)
+    acc_t = torch.float64 if dtype == torch.float64 else torch.float32
+    acc = (torch.randn(n, generator=g, dtype=torch.float64) * 3).to(dev, acc_t)
+    ref = acc.clone()
+    lib = _abi.load()
+    for _ in range(2):
+        part = (torch.randn(n, generator=g, dtype=torch.float64) * 7).to(dev, dtype)
+        ref += part.to(acc_t)
+        _abi.check(lib.tnce_accumulate(ctypes.c_void_p(acc.data_ptr()), ctypes.c_void_p(part.data_ptr()),
+                                       _DTYPES[dtype], n, ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)),
+                   "accumulate")
+    torch.cuda.synchronize()
+    assert torch.equal(acc, ref)
