@@ -55,7 +55,8 @@ typedef struct {
  * over every token (padding included), pairs = 2 for signed_product / lower_degree_mix and 1 otherwise: the two
  * factors of the reference's Cauchy-Schwarz score bound max|S| <= max|q| max|k| / sqrt(dk)
  * (ref: tnlm/model.py:33-38,83-85), taken from the rows the forward kernel reads anyway.
- * rope_cos / rope_sin (optional, both or neither): per-token rotary tables, (B, T, dk/2) fp32 contiguous, as the
+ * rope_cos / rope_sin (optional, both or neither): per-token rotary tables, (B, T, dk/2) fp32 contiguous and
+ * 16-byte aligned, as the
  * reference's rope_tables builds them (ref: tnlm/attention.py:41-45; its (B, 1, T, dk/2) layout is the same memory).
  * With them, q1/k1 (q2/k2) are the inputs already rotated by these tables (tnpa_rope), tnpa_forward is unchanged,
  * and tnpa_backward returns dq/dk with respect to the unrotated inputs: the gradient of the rotation is applied to
@@ -106,7 +107,8 @@ int tnpa_doc_bounds(const void* doc_ids, int32_t doc_is_int64, int64_t doc_strid
                     int32_t seq_len, int32_t* doc_start, int32_t* query_end, void* stream);
 
 /* Rotary position embedding of one (B,H,T,d) tensor x into out (same shape and dtype; out may be x itself) by
- * per-token tables cos / sin, (B, T, d/2) fp32 contiguous (ref: tnlm/attention.py:41-45). One pass, in fp32 with
+ * per-token tables cos / sin, (B, T, d/2) fp32 contiguous, 16-byte aligned (ref: tnlm/attention.py:41-45). One
+ * pass, in fp32 with
  * x1 = x[..., :d/2], x2 = x[..., d/2:]: inverse = 0 gives out = (x1 cos - x2 sin, x1 sin + x2 cos), the reference's
  * apply_rope (ref: tnlm/attention.py:48-51, called at ref: tnlm/model.py:70-71,81-82); inverse = 1 gives the
  * gradient of that rotation with respect to its input, g -> (g1 cos + g2 sin, g2 cos - g1 sin). Every product and

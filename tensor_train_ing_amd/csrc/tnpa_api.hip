@@ -105,6 +105,8 @@ int check_problem(const tnpa_problem_t* pp) {
     return fail(TNPA_ERR_INVALID, "offset_square needs offset (H)");
   if ((p.rope_cos == nullptr) != (p.rope_sin == nullptr))
     return fail(TNPA_ERR_INVALID, "rope_cos and rope_sin: both or neither");
+  if (((uintptr_t)p.rope_cos) % 16 != 0 || ((uintptr_t)p.rope_sin) % 16 != 0)
+    return fail(TNPA_ERR_INVALID, "rope_cos / rope_sin must be 16-byte aligned");
   return TNPA_OK;
 }
 
@@ -651,6 +653,8 @@ int tnpa_rope(const tnpa_tensor_t* x, const tnpa_tensor_t* out, int32_t batch, i
               int32_t head_dim, int32_t dtype, const float* cos, const float* sin, int32_t inverse, void* stream) {
   if (x == nullptr || out == nullptr || cos == nullptr || sin == nullptr)
     return fail(TNPA_ERR_INVALID, "tnpa_rope: null pointer");
+  if (((uintptr_t)cos) % 16 != 0 || ((uintptr_t)sin) % 16 != 0)
+    return fail(TNPA_ERR_INVALID, "tnpa_rope: cos / sin must be 16-byte aligned");
   if (batch <= 0 || heads <= 0 || seq_len <= 0) return fail(TNPA_ERR_INVALID, "tnpa_rope: sizes must be positive");
   if (!valid_dim(head_dim)) return fail(TNPA_ERR_INVALID, "tnpa_rope: head dim must be a power of 2 >= 16");
   if (dtype != TNPA_BF16 && dtype != TNPA_F32 && dtype != TNPA_F16)

@@ -121,6 +121,12 @@ def test_misaligned_views_and_missing_parameters_are_rejected(lib):
     p = _problem(kind=_abi.LOWER_DEGREE_MIX)
     assert lib.tnpa_forward(ctypes.byref(p), ctypes.byref(out), None) == _abi.ERR_INVALID
     assert "coef" in lib.tnpa_last_error().decode()
+    p = _problem(rope_cos=4096 + 8, rope_sin=8192)
+    assert lib.tnpa_forward(ctypes.byref(p), ctypes.byref(out), None) == _abi.ERR_INVALID
+    assert "aligned" in lib.tnpa_last_error().decode()
+    assert lib.tnpa_rope(ctypes.byref(out), ctypes.byref(out), 2, 2, 128, 64, _abi.BF16, ctypes.c_void_p(4100),
+                         ctypes.c_void_p(4096), 0, None) == _abi.ERR_INVALID
+    assert "aligned" in lib.tnpa_last_error().decode()
     p = _problem(kind=_abi.OFFSET_SQUARE)
     assert lib.tnpa_forward(ctypes.byref(p), ctypes.byref(out), None) == _abi.ERR_INVALID
     assert "offset" in lib.tnpa_last_error().decode()
