@@ -123,6 +123,16 @@ def event_intervals(fn, reps):
     return [evs[i].elapsed_time(evs[i + 1]) for i in range(reps)]
 
 
+def median_back_to_back(fn, reps):
+    """Median interval (ms) of fn run reps times back to back, a HIP event between consecutive runs (after 3 untimed
+    runs): each launch's time in the steady state of a busy GPU, as inside the step."""
+    import torch
+    for _ in range(3):
+        fn()
+    torch.cuda.synchronize()
+    return statistics.median(event_intervals(fn, reps))
+
+
 def median_each(fn, reps):
     """Median duration (ms) of fn over reps runs, each bracketed by its own event pair (after 3 untimed runs)."""
     import torch
@@ -141,8 +151,8 @@ def median_each(fn, reps):
 
 
 def kernel_times(kind, q, k, q2, k2, v, do, doc, rs, degree, reps):
-    """Median duration (ms) of each launch of the step, timed alone with HIP events on the stream the library
-    launches on (torch's current stream): the forward, then each launch of the backward plan in order (the
+    """Median duration (ms) of each launch of the step, repeated back to back with HIP events on the stream the
+    library launches on (torch's current stream): the forward, then each launch of the backward plan in order (the
     library's internal launch-level entry point; a launch run alone reads what the earlier ones wrote)."""
     import torch
     from tensor_train_ing_amd import _abi
@@ -166,12 +176,12 @@ def kernel_times(kind, q, k, q2, k2, v, do, doc, rs, degree, reps):
                        ws.data_ptr(), nbytes)
     st = _stream(q.device)
     od = _desc(o)
-    out = {"fwd": median_each(
+    out = {"fwd": median_back_to_back(
         lambda: _abi.check(lib.tnpa_forward(ctypes.byref(prob), ctypes.byref(od), st), "fwd"), reps)}
     _abi.check(lib.tnpa_backward(ctypes.byref(prob), ctypes.byref(grads), st), "bwd")  # fills the workspace
     for i in range(lib.tnpa_x_launches(ctypes.byref(prob), 0)):
         name = lib.tnpa_x_launch_name(ctypes.byref(prob), 0, i).decode()
-        out[name] = median_each(
+        out[name] = median_back_to_back(
             lambda: _abi.check(lib.tnpa_x_backward(ctypes.byref(prob), ctypes.byref(grads), 0, i, st), name), reps)
     return out
 
@@ -368,7 +378,9 @@ def main(argv=None):
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
-    ap.add_argument("--warmup", type=int, default=10)
+    # a fresh process reaches its steady step time only after ~70 steps (0.74 ms per step at steps 10-19, 0.67 from
+    # step 80 on, at the headline), so the default warmup covers that
+    ap.add_argument("--warmup", type=int, default=100)
     ap.add_argument("--config", default="1b", choices=sorted(CONFIGS))
     ap.add_argument("--kind", default="power", choices=sorted(KIND_CODES),
                     help="polynomial family (default: power, the degree-p kind BASELINE.json's configs name; "
@@ -465,6 +477,9 @@ def main(argv=None):
                      "rope_kernel_ms_per_tensor": round(median_each(lambda: rope_rotate(qd, cs, sn), a.kernel_reps),
                                                         4)}
 
+    kt = kernel_times(kind, q.detach(), k.detach(), q2.detach() if two else None, k2.detach() if two else None,
+                      v.detach(), do, doc, rs, degree, a.kernel_reps)
+
     # counted FLOPs (exact causal pairs): one q/k pair fwd 2 matmul units of 2*B*H*Npairs*D, fwd+bwd 7; two pairs
     # fwd 3 (S1, S2, PV), fwd+bwd 11
     unit = 2.0 * B * H * npairs(T, a.doc_len) * D
@@ -473,8 +488,6 @@ def main(argv=None):
     value = fl_step / (ms * 1e-3) / 1e12
     peak = PEAKS[a.dtype]
 
-    kt = kernel_times(kind, q.detach(), k.detach(), q2.detach() if two else None, k2.detach() if two else None,
-                      v.detach(), do, doc, rs, degree, a.kernel_reps)
     units = UNITS_TWO if two else UNITS_ONE
     dom = max(kt, key=lambda n: kt[n])
     ach = units[dom] * unit / (kt[dom] * 1e-3) / 1e12
