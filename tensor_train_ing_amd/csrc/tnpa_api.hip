@@ -442,9 +442,12 @@ __global__ void k_dpar_reduce(const float* part, int B, int H, int NNB, float* o
 //   kv     the combined dK/dV kernel (the wave-pair kernel for 16-bit, one q/k pair, head dims 128), or dv and
 //          dk: the two passes of the split key side (16-bit, one q/k pair, other head dims above 64)
 //   q      the dQ kernel (recomputes S and dP)
-//   qds    dQ = dS K from the dS tiles the dk pass stored in the workspace (16-bit, one q/k pair, head dim 128,
-//          unless TNPA_X_DS_OFF or the tiles would exceed kMaxDsTileBytes): one matrix product instead of three
+//   qds    dQ = dS K from the dS tiles the key side stored in the workspace (16-bit, key head dim 128, unless
+//          TNPA_X_DS_OFF or the tiles would exceed kMaxDsTileBytes): one matrix product instead of three; two
+//          q/k pairs run it once per pair (dQ1 = dS1 K1, dQ2 = dS2 K2)
 //   dpar   the fixed-order dcoef/db reduction of the per-key-block partials (offset_square, lower_degree_mix)
+//   rope   with rotary tables, the rotation's gradient on dK in place, where the key side writes dK from its
+//          accumulators (two q/k pairs, head dim 16); the dQ and the other dK epilogues apply it themselves
 enum LaunchKind { L_SCALE = 0, L_KV = 1, L_DV = 2, L_DK = 3, L_Q = 4, L_DPAR = 5, L_QDS = 6, L_ROPE = 7 };
 const char* const kLaunchNames[] = {"scale", "kv", "dv", "dk", "q", "dpar", "qds", "rope"};
 
