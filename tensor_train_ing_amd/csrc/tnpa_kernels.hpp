@@ -1691,7 +1691,8 @@ k_bwd_kv_pair(const KParams p) {
 }
 
 // ------------------------------------------------------------------------------------------------ dQ from dS
-// dQ = gf * dS K from the dS tiles the dK pass stored: one matrix product per (query, key) sub-block instead of the
+// dQ = gf * dS K from the dS tiles the key side stored (for two q/k pairs the host launches it once per pair, with
+// K2 / dS2 / dQ2 in place of K1 / dS1 / dQ1): one matrix product per (query, key) sub-block instead of the
 // S and dP recompute of k_bwd_q. A workgroup owns BM = NW*32 queries; wave w accumulates dQ^T = K^T dS^T for its
 // 32-query subtile (lane <-> query). K tiles of BN keys go through three LDS buffers shared by the workgroup (one
 // barrier per tile); each wave's dS tiles come from global memory straight into registers two tiles ahead, then
