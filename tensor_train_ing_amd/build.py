@@ -28,7 +28,7 @@ COMMON = [f"--offload-arch={ARCH}", "-O3", "-std=c++17", "-fPIC", "-Wall", "-Wno
           "-Wno-unused-but-set-variable", "-Wno-unknown-pragmas", *DEVICE_FLAGS]
 
 ELEMENT_TYPES = {"bf16": "__bf16", "f16": "_Float16", "f32": "float"}
-HEAD_DIMS = (16, 32, 64, 128)
+HEAD_DIMS = (16, 32, 64, 128, 256)
 HEADERS = ("tnpa_device.hpp", "tnpa_kernels.hpp", "tnpa_params.hpp", "tnpa_internal.h", "tnpa_error.hpp")
 
 

@@ -68,6 +68,7 @@ int check_tensor(const tnpa_tensor_t& t, const char* name, const tnpa_problem_t&
 }
 
 bool two_pairs(int kind) { return kind == TNPA_SIGNED_PRODUCT || kind == TNPA_LOWER_DEGREE_MIX; }
+int poly_of(const tnpa_problem_t& p);
 
 int check_problem(const tnpa_problem_t* pp) {
   if (pp == nullptr) return fail(TNPA_ERR_INVALID, "null problem");
@@ -77,14 +78,17 @@ int check_problem(const tnpa_problem_t* pp) {
                 p.seq_len);
   if (!valid_dim(p.head_dim_k) || !valid_dim(p.head_dim_v))
     return fail(TNPA_ERR_INVALID, "head dims: powers of 2 >= 16 (got dk=%d, dv=%d)", p.head_dim_k, p.head_dim_v);
-  if (p.head_dim_k > 128 || p.head_dim_v > 128)
-    return fail(TNPA_ERR_UNSUPPORTED, "head dims above 128 are not built (got dk=%d, dv=%d)", p.head_dim_k,
+  if (p.head_dim_k > 256 || p.head_dim_v > 256)
+    return fail(TNPA_ERR_UNSUPPORTED, "head dims above 256 are not built (got dk=%d, dv=%d)", p.head_dim_k,
                 p.head_dim_v);
   if (p.kind < 0 || p.kind > 3) return fail(TNPA_ERR_INVALID, "unknown kind %d", p.kind);
   if (p.kind == TNPA_POWER && (p.degree < 1 || p.degree > 8))
     return fail(TNPA_ERR_INVALID, "power kind needs degree in 1..8 (got %d)", p.degree);
   if (p.dtype != TNPA_BF16 && p.dtype != TNPA_F32 && p.dtype != TNPA_F16)
     return fail(TNPA_ERR_INVALID, "unknown dtype %d", p.dtype);
+  if (!tnpa::dims_built(p.dtype == TNPA_F32, poly_of(p), p.head_dim_k, p.head_dim_v))
+    return fail(TNPA_ERR_UNSUPPORTED, "fp32 with two q/k pairs is built for head dims up to 128 (got dk=%d, dv=%d)",
+                p.head_dim_k, p.head_dim_v);
   const long long blocks = (long long)p.batch * p.heads * ((p.seq_len + 31) / 32);
   if (blocks > 0x7fffffffLL) return fail(TNPA_ERR_UNSUPPORTED, "problem too large for one launch");
   const int es = esize(p.dtype);
@@ -164,8 +168,8 @@ hipError_t run_dims(int ph, int dk, int dv, const tnpa::KParams& k, hipStream_t 
     return ph == PH_FWD      ? tnpa::launch_fwd<T, POLY, DK_, DV_>(k, s)                      \
            : ph == PH_BWD_KV ? tnpa::launch_bwd_kv<T, POLY, DK_, DV_>(k, s)                   \
                              : tnpa::launch_bwd_q<T, POLY, DK_, DV_>(k, s);
-#define TNPA_ROW(DK_) TNPA_CASE(DK_, 16) TNPA_CASE(DK_, 32) TNPA_CASE(DK_, 64) TNPA_CASE(DK_, 128)
-  TNPA_ROW(16) TNPA_ROW(32) TNPA_ROW(64) TNPA_ROW(128)
+#define TNPA_ROW(DK_) TNPA_CASE(DK_, 16) TNPA_CASE(DK_, 32) TNPA_CASE(DK_, 64) TNPA_CASE(DK_, 128) TNPA_CASE(DK_, 256)
+  TNPA_ROW(16) TNPA_ROW(32) TNPA_ROW(64) TNPA_ROW(128) TNPA_ROW(256)
 #undef TNPA_ROW
 #undef TNPA_CASE
   return hipErrorInvalidValue;
@@ -482,9 +486,9 @@ int make_plan(const tnpa_problem_t& p, int opts, Plan& pl) {
   const int64_t dos_bytes = pl.prescale ? (int64_t)p.batch * p.heads * p.seq_len * dv * esize(p.dtype) : 0;
   const int64_t ds_bytes = tnpa::ds_tile_bytes(p.batch, p.heads, p.seq_len, esize(p.dtype));
   // dS tiles (one set per q/k pair) where the key side forms dS in a dK pass (one pair) or in the combined kernel
-  // (two pairs), for 16-bit inputs at key head dim 128
+  // (two pairs; their split passes at head dims above 128 store none), for 16-bit inputs at key head dim 128
   const int npairs = tnpa::two_pair_poly(poly) ? 2 : 1;
-  pl.ds = (split || npairs == 2) && !f32 && dk == 128 && !(opts & TNPA_X_DS_OFF) &&
+  pl.ds = (npairs == 1 ? split : !split) && !f32 && dk == 128 && !(opts & TNPA_X_DS_OFF) &&
           npairs * ds_bytes <= kMaxDsTileBytes;
   pl.dpar_off = 0;
   pl.dos_off = align256(dpar_bytes);

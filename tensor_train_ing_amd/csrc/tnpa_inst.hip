@@ -1,5 +1,5 @@
 // Explicit instantiation unit: compiled once per (element type, key head dim) with
-//   -DTNPA_INST_T=<__bf16|_Float16|float> -DTNPA_INST_DK=<16|32|64|128>
+//   -DTNPA_INST_T=<__bf16|_Float16|float> -DTNPA_INST_DK=<16|32|64|128|256>
 // so that the kernel variants build in parallel translation units.
 #include "tnpa_kernels.hpp"
 
@@ -15,7 +15,8 @@ namespace tnpa {
   template hipError_t launch_fwd<TNPA_INST_T, POLY, TNPA_INST_DK, DV>(const KParams&, hipStream_t);        \
   template hipError_t launch_bwd_kv<TNPA_INST_T, POLY, TNPA_INST_DK, DV>(const KParams&, hipStream_t);        \
   template hipError_t launch_bwd_q<TNPA_INST_T, POLY, TNPA_INST_DK, DV>(const KParams&, hipStream_t);
-#define TNPA_INST_DVS(POLY) TNPA_INST(POLY, 16) TNPA_INST(POLY, 32) TNPA_INST(POLY, 64) TNPA_INST(POLY, 128)
+#define TNPA_INST_DVS(POLY) \
+  TNPA_INST(POLY, 16) TNPA_INST(POLY, 32) TNPA_INST(POLY, 64) TNPA_INST(POLY, 128) TNPA_INST(POLY, 256)
 TNPA_INST_DVS(POLY_GEN1)
 TNPA_INST_DVS(POLY_GEN2)
 TNPA_INST_DVS(POLY_POW2)

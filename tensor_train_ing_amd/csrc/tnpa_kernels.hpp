@@ -171,8 +171,11 @@ __host__ __device__ constexpr int cmax(int a, int b) { return a > b ? a : b; }
 template <typename T, int POLY, int DK, int DV> struct Cfg {
   static constexpr bool F32 = sizeof(T) == 4;
   static constexpr int NPAIR = two_pair_poly(POLY) ? 2 : 1;
+  // Head dims above 128: four-wave workgroups at one wave per SIMD (a wave's 32 rows of operands and accumulators
+  // take 128 registers per 256 columns), 32-row tiles, and the key side as separate dV and dK passes.
+  static constexpr bool BIG = big_dims(DK, DV);
   // two waves per SIMD (16-bit, one pair): eight waves per workgroup, so each staged tile serves 256 rows
-  static constexpr bool TWO = !F32 && NPAIR == 1;
+  static constexpr bool TWO = !F32 && NPAIR == 1 && !BIG;
   // Head dims up to 64: four-wave workgroups, two per CU (their LDS fits twice), so one workgroup's barrier waits,
   // prologue and epilogue overlap the other's MFMA work. Larger head dims: one eight-wave workgroup per CU.
   static constexpr bool SMALL = TWO && DK <= 64 && DV <= 64;
@@ -182,20 +185,21 @@ template <typename T, int POLY, int DK, int DV> struct Cfg {
   // (two staging buffers; 16 registers spilled, still 19% faster than one wave per SIMD); lower_degree_mix's would
   // spill 315 registers and its dQ kernels would not fit either, so those stay at one wave per SIMD.
   static constexpr bool PAIR2_TWO = !F32 && NPAIR == 2 && DK <= 64 && DV <= 64;
-  static constexpr bool FW2 = PAIR2_TWO || (!F32 && POLY == POLY_SP);
+  static constexpr bool FW2 = PAIR2_TWO || (!F32 && POLY == POLY_SP && !BIG);
   // (the two-pair forward up to head dim 64 in four-wave workgroups, two per CU with two staging buffers each: 10%
   // faster than one eight-wave workgroup; the two-pair dQ kernel measured no better that way)
-  static constexpr int FW_NW = TWO ? NW2 : PAIR2_TWO ? 4 : FW2 ? 8 : 4, FW_QW = 1, FW_BN = F32 ? 32 : 64;
+  static constexpr int FW_NW = TWO ? NW2 : PAIR2_TWO ? 4 : FW2 ? 8 : 4, FW_QW = 1, FW_BN = F32 || BIG ? 32 : 64;
   static constexpr int FW_WPE = TWO || FW2 ? 2 : 1;
-  static constexpr int BQ_NW = TWO ? NW2 : PAIR2_TWO ? 8 : 4, BQ_QW = 1, BQ_BN = F32 ? 32 : 64;
+  static constexpr int BQ_NW = TWO ? NW2 : PAIR2_TWO ? 8 : 4, BQ_QW = 1, BQ_BN = F32 || BIG ? 32 : 64;
   static constexpr int BQ_WPE = TWO || PAIR2_TWO ? 2 : 1;
   // Key side: separate dV and dK passes at two waves per SIMD for head dim 128 (one kernel holding dK, dV, K and V
   // would need 376 registers there); up to 64 the combined kernel fits 256 registers and saves the S recompute.
-  static constexpr bool KV_SPLIT = TWO && !SMALL;
+  static constexpr bool KV_SPLIT = (TWO && !SMALL) || BIG;
   // (two pairs at head dim 128: 32-query tiles, whose operand reads the compiler keeps in flight fit the one-wave
   // kernel's 512 registers without spills; 64-query tiles spilled 13 registers and ran 20% slower)
-  static constexpr int KV_NW = KV_SPLIT ? NW2 : 4, KV_KW = 1, KV_BM = F32 || (NPAIR == 2 && DK > 64) ? 32 : 64;
-  static constexpr int KV_WPE = SMALL ? 2 : 1;
+  static constexpr int KV_NW = KV_SPLIT && !BIG ? NW2 : 4, KV_KW = 1;
+  static constexpr int KV_BM = F32 || BIG || (NPAIR == 2 && DK > 64) ? 32 : 64;
+  static constexpr int KV_WPE = SMALL ? 2 : 1, KV_SPLIT_WPE = BIG ? 1 : 2;
   static constexpr int KV_KEYS = KV_NW * KV_KW * 32;
 };
 
@@ -1843,16 +1847,21 @@ k_bwd_q_ds(const KParams p) {
 
 // ------------------------------------------------------------------------------------------------ launchers
 template <typename T, int POLY, int DK, int DV> hipError_t launch_fwd(const KParams& p, hipStream_t st) {
+  if constexpr (!dims_built(sizeof(T) == 4, POLY, DK, DV)) return hipErrorInvalidValue;
+  else {
   typedef Cfg<T, POLY, DK, DV> C;
   constexpr int BM = C::FW_NW * C::FW_QW * 32;
   const int grid = p.B * p.H * ((p.T + BM - 1) / BM);
   hipLaunchKernelGGL((k_fwd<T, POLY, DK, DV, C::FW_NW, C::FW_QW, C::FW_BN, C::FW_WPE>), dim3(grid), dim3(C::FW_NW * 64), 0, st, p);
   return hipGetLastError();
+  }
 }
 
 template <typename T, int POLY, int DK, int DV> hipError_t launch_bwd_kv(const KParams& p, hipStream_t st) {
+  if constexpr (!dims_built(sizeof(T) == 4, POLY, DK, DV)) return hipErrorInvalidValue;
+  else {
   typedef Cfg<T, POLY, DK, DV> C;
-  static_assert(C::KV_KEYS == (C::KV_SPLIT ? 256 : 128), "dK/dV block size mirrors kv_block_keys()");
+  static_assert(C::KV_KEYS == (C::KV_SPLIT && !C::BIG ? 256 : 128), "dK/dV block size mirrors kv_block_keys()");
   if constexpr (kv_pair_cfg<T, POLY, DK, DV>()) {
     const int grid = p.B * p.H * ((p.T + 127) / 128);
     hipLaunchKernelGGL((k_bwd_kv_pair<T, POLY, DK, DV>), dim3(grid), dim3(512), 0, st, p);
@@ -1861,25 +1870,29 @@ template <typename T, int POLY, int DK, int DV> hipError_t launch_bwd_kv(const K
   const int grid = p.B * p.H * ((p.T + C::KV_KEYS - 1) / C::KV_KEYS);
   if constexpr (C::KV_SPLIT) {
     if (p.kvsel & 1)
-      hipLaunchKernelGGL((k_bwd_kv<T, POLY, DK, DV, C::KV_NW, C::KV_KW, C::KV_BM, 2, KV_DV>), dim3(grid),
+      hipLaunchKernelGGL((k_bwd_kv<T, POLY, DK, DV, C::KV_NW, C::KV_KW, C::KV_BM, C::KV_SPLIT_WPE, KV_DV>), dim3(grid),
                          dim3(C::KV_NW * 64), 0, st, p);
     if (p.kvsel & 2)
-      hipLaunchKernelGGL((k_bwd_kv<T, POLY, DK, DV, C::KV_NW, C::KV_KW, C::KV_BM, 2, KV_DK>), dim3(grid),
+      hipLaunchKernelGGL((k_bwd_kv<T, POLY, DK, DV, C::KV_NW, C::KV_KW, C::KV_BM, C::KV_SPLIT_WPE, KV_DK>), dim3(grid),
                          dim3(C::KV_NW * 64), 0, st, p);
   } else {
     hipLaunchKernelGGL((k_bwd_kv<T, POLY, DK, DV, C::KV_NW, C::KV_KW, C::KV_BM, C::KV_WPE, KV_BOTH>), dim3(grid),
                        dim3(C::KV_NW * 64), 0, st, p);
   }
   return hipGetLastError();
+  }
 }
 
 template <typename T, int POLY, int DK, int DV> hipError_t launch_bwd_q(const KParams& p, hipStream_t st) {
+  if constexpr (!dims_built(sizeof(T) == 4, POLY, DK, DV)) return hipErrorInvalidValue;
+  else {
   typedef Cfg<T, POLY, DK, DV> C;
   constexpr int BM = C::BQ_NW * C::BQ_QW * 32;
   const int grid = p.B * p.H * ((p.T + BM - 1) / BM);
   hipLaunchKernelGGL((k_bwd_q<T, POLY, DK, DV, C::BQ_NW, C::BQ_QW, C::BQ_BN, C::BQ_WPE>), dim3(grid), dim3(C::BQ_NW * 64), 0, st,
                      p);
   return hipGetLastError();
+  }
 }
 
 template <typename T, int DK> hipError_t launch_bwd_q_ds(const KParams& p, hipStream_t st) {

@@ -45,10 +45,17 @@ struct KParams {
   float gf;  // factor on dQ and dK (p*sm^p, sm^2 or sm)
 };
 
-// Whether the key side runs as separate dV and dK passes (16-bit inputs, one q/k pair, a head dim above 64);
-// mirrors Cfg::KV_SPLIT.
+// Head dims above 128 (256): one wave per SIMD, 32-row tiles, split key side (Cfg::BIG).
+__host__ __device__ constexpr bool big_dims(int dk, int dv) { return dk > 128 || dv > 128; }
+
+// Whether kernels are built for these head dims (powers of two from 16 to 256 otherwise): not fp32 with two q/k
+// pairs above head dim 128, whose two K tiles and V tile of 32 rows at 1 KB each exceed LDS at two buffers.
+constexpr bool dims_built(bool f32, int poly, int dk, int dv) { return !(f32 && two_pair_poly(poly) && big_dims(dk, dv)); }
+
+// Whether the key side runs as separate dV and dK passes (16-bit inputs, one q/k pair, a head dim above 64; any
+// input with a head dim above 128); mirrors Cfg::KV_SPLIT.
 inline bool kv_split(bool f32, int poly, int dk, int dv) {
-  return !f32 && !two_pair_poly(poly) && (dk > 64 || dv > 64);
+  return big_dims(dk, dv) || (!f32 && !two_pair_poly(poly) && (dk > 64 || dv > 64));
 }
 
 // Whether the key side is the wave-pair kernel k_bwd_kv_pair (16-bit inputs, one q/k pair, head dims 128): one launch
@@ -61,25 +68,26 @@ template <typename T, int POLY, int DK, int DV> constexpr bool kv_pair_cfg() {
 }
 
 // Whether the key side writes dK as whole rows from LDS, where its epilogue applies the gradient of a rotary
-// embedding (copy_out_rope): one q/k pair and no padded head dim. The two-pair and head-dim-16 key sides store dK
-// from the accumulators, and the backward rotates it in a pass after them. (Every dQ kernel writes whole rows.)
+// embedding (copy_out_rope): one q/k pair and no padded head dim (fp32 at head dim 256: its K and V rows do not fit
+// LDS together). The other key sides store dK from the accumulators, and the backward rotates it in a pass after
+// them. (Every dQ kernel writes whole rows.)
 constexpr bool rope_dk_epilogue(bool f32, int poly, int dk, int dv) {
-  return !two_pair_poly(poly) && dk >= 32 && dv >= 32;
+  return !two_pair_poly(poly) && dk >= 32 && dv >= 32 && !(f32 && big_dims(dk, dv));
 }
 
 // Keys per dK/dV workgroup (sizes the dcoef/db partials); mirrors Cfg::KV_KEYS: eight waves of 32 keys for the split
-// passes, four waves (or four wave pairs) for the combined kernels.
+// passes up to head dim 128, four waves (or four wave pairs) otherwise.
 inline int kv_block_keys(bool f32, int poly, int dk, int dv) {
-  return kv_split(f32, poly, dk, dv) && !kv_pair(f32, poly, dk, dv) ? 256 : 128;
+  return kv_split(f32, poly, dk, dv) && !kv_pair(f32, poly, dk, dv) && !big_dims(dk, dv) ? 256 : 128;
 }
 
 // Whether the dK/dV passes scale dO by the row scale themselves at no cost: they stage the dO rows a step ahead and
 // apply the factor when writing them to LDS (three-buffer staging; 16-bit inputs, one q/k pair, and 64-row tiles
 // of q and dO that split into whole 16-byte chunks per thread: 8*d chunks over 256 threads for head dims up to 64,
-// 512 threads above). Then a separate pre-scaling pass costs more than it saves. Mirrors k_bwd_kv's NBUF == 3.
+// 512 threads up to 128). Then a separate pre-scaling pass costs more than it saves. Mirrors k_bwd_kv's NBUF == 3.
 constexpr bool kv_scales_in_pass(bool f32, int poly, int dk, int dv) {
   const int nt = dk <= 64 && dv <= 64 ? 256 : 512;
-  return !f32 && !two_pair_poly(poly) && (8 * dk) % nt == 0 && (8 * dv) % nt == 0;
+  return !f32 && !two_pair_poly(poly) && !big_dims(dk, dv) && (8 * dk) % nt == 0 && (8 * dv) % nt == 0;
 }
 
 // dS tiles: the masked, row-scaled gradient dS of every 32x32 (query, key) sub-block i >= j of one (b, h) head,

@@ -94,7 +94,8 @@ def _problem(**kw):
     ("batch", 0, 1, "positive"),
     ("head_dim_k", 24, 1, "powers of 2"),
     ("head_dim_v", 8, 1, "powers of 2"),
-    ("head_dim_k", 256, 2, "above 128"),
+    ("head_dim_k", 512, 2, "above 256"),
+    ("head_dim_v", 512, 2, "above 256"),
     ("kind", 7, 1, "unknown kind"),
     ("degree", 0, 1, "degree"),
     ("dtype", 9, 1, "dtype"),
@@ -108,6 +109,20 @@ def test_forward_rejects_bad_arguments_before_launch(lib, field, value, code, ms
     out = _abi.Tensor(4096, 2 * 128 * 64, 128 * 64, 64)
     assert lib.tnpa_forward(ctypes.byref(p), ctypes.byref(out), None) == code
     assert msg in lib.tnpa_last_error().decode()
+
+
+def test_fp32_two_pairs_above_head_dim_128_unsupported(lib):
+    """fp32 with two q/k pairs is built up to head dim 128 (its tiles would not fit LDS): TNPA_ERR_UNSUPPORTED
+    (ValueError) before anything is launched; one pair, or 16-bit, at 256 is accepted."""
+    from tensor_train_ing_amd import _abi
+    for kind in (_abi.SIGNED_PRODUCT, _abi.LOWER_DEGREE_MIX):
+        p = _problem(kind=kind, dtype=_abi.F32, head_dim_k=256, coef=4096)
+        assert lib.tnpa_x_launches(ctypes.byref(p), 0) == -1
+        out = _abi.Tensor(4096, 2 * 128 * 64, 128 * 64, 64)
+        assert lib.tnpa_forward(ctypes.byref(p), ctypes.byref(out), None) == _abi.ERR_UNSUPPORTED
+        assert "up to 128" in lib.tnpa_last_error().decode()
+    assert lib.tnpa_x_launches(ctypes.byref(_problem(kind=_abi.SIGNED_PRODUCT, head_dim_k=256)), 0) == 4
+    assert lib.tnpa_x_launches(ctypes.byref(_problem(dtype=_abi.F32, head_dim_k=256, head_dim_v=256)), 0) == 4
 
 
 def test_misaligned_views_and_missing_parameters_are_rejected(lib):
@@ -231,6 +246,21 @@ def test_backward_plan(lib):
     for kw in (dict(head_dim_k=16, head_dim_v=16), dict(kind=_abi.LOWER_DEGREE_MIX, coef=4096),
                dict(kind=_abi.SIGNED_PRODUCT, head_dim_k=128, head_dim_v=128)):
         assert _launches(lib, _problem(rope_cos=4096, rope_sin=8192, **kw)) == _launches(lib, _problem(**kw)) + ["rope"]
+    # head dims above 128: the row-scaled dO, then separate dV and dK passes of 128 keys, for every dtype and kind;
+    # dQ from dS tiles for one 16-bit pair at key head dim 128 (the dK pass stores them), else recomputing S and dP;
+    # the dK epilogue rotates except for fp32 (a pass after)
+    for kw in (dict(head_dim_k=256, head_dim_v=256), dict(head_dim_k=256, head_dim_v=64),
+               dict(dtype=_abi.F32, head_dim_k=16, head_dim_v=256), dict(dtype=_abi.F32, head_dim_k=128, head_dim_v=256),
+               dict(kind=_abi.SIGNED_PRODUCT, head_dim_k=256, head_dim_v=128),
+               dict(kind=_abi.SIGNED_PRODUCT, head_dim_k=128, head_dim_v=256)):
+        assert _launches(lib, _problem(**kw)) == ["scale", "dv", "dk", "q"]
+    assert _launches(lib, _problem(head_dim_k=128, head_dim_v=256)) == ["scale", "dv", "dk", "qds"]
+    assert _launches(lib, _problem(kind=_abi.OFFSET_SQUARE, offset=4096, head_dim_k=256)) == [
+        "scale", "dv", "dk", "q", "dpar"]
+    assert _launches(lib, _problem(rope_cos=4096, rope_sin=8192, head_dim_k=256, head_dim_v=256)) == [
+        "scale", "dv", "dk", "q"]
+    assert _launches(lib, _problem(rope_cos=4096, rope_sin=8192, dtype=_abi.F32, head_dim_k=256)) == [
+        "scale", "dv", "dk", "q", "rope"]
     assert lib.tnpa_x_launch_name(ctypes.byref(_problem()), 0, 5) == b""
 
 

@@ -367,6 +367,31 @@ def test_small_head_dim_block_counts(B, H, T):
     _check(compare(res, ref), BF16_FRO, BF16_MAX)
 
 
+# ------------------------------------------------------------------ head dims above 128
+# Four-wave blocks at one wave per SIMD, 32-row tiles, separate dV and dK passes of 128 keys; dQ from dS tiles for
+# one 16-bit pair at key head dim 128, else recomputing S and dP. Documents, padding, odd lengths, mixed dk/dv.
+@pytest.mark.parametrize("kind", ["power", "offset_square", "signed_product", "lower_degree_mix"])
+@pytest.mark.parametrize("dk,dv", [(256, 256), (256, 64), (128, 256), (32, 256)])
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_head_dim_256_16bit(kind, dk, dv, dtype):
+    B, H, T = 2, 2, 333
+    print(f"[head dim 256] kind={kind} dk={dk} dv={dv} dtype={dtype} B{B} H{H} T{T}", flush=True)
+    res, ref = _case(kind, B, H, T, dk, dv, dtype, docs=_doc_rows(B, T), degree=2 if kind == "power" else None,
+                     qk_scale=dk ** -0.25, seed=dk + 3 * dv)
+    _check(compare(res, ref), BF16_FRO, BF16_MAX)
+
+
+@pytest.mark.parametrize("kind", ["power", "offset_square"])
+@pytest.mark.parametrize("dk,dv", [(256, 256), (256, 32), (64, 256)])
+def test_head_dim_256_fp32(kind, dk, dv):
+    """fp32 at the reference's 2e-4 gate (one q/k pair; fp32 with two pairs is built up to head dim 128)."""
+    B, H, T = 1, 2, 150
+    print(f"[head dim 256 fp32] kind={kind} dk={dk} dv={dv}", flush=True)
+    res, ref = _case(kind, B, H, T, dk, dv, torch.float32, docs=_doc_rows(B, T), degree=2 if kind == "power" else None,
+                     seed=7)
+    _check(compare(res, ref), F32_FRO)
+
+
 def test_d128_bthd_layout():
     """(B, T, H, d) storage, the model's layout: time stride H*d, read in place."""
     res, ref = _case("power", 2, 4, 200, 128, 128, torch.bfloat16, docs=_doc_rows(2, 200), degree=2,

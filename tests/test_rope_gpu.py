@@ -56,11 +56,13 @@ def test_rope_kernel_matches_reference_apply_rope(dtype, D, layout):
                                              ("offset_square", torch.float16, 128, 160),
                                              ("signed_product", torch.bfloat16, 128, 250),
                                              ("lower_degree_mix", torch.bfloat16, 64, 130),
-                                             ("power", torch.float32, 32, 100), ("power", torch.bfloat16, 16, 90)])
+                                             ("power", torch.float32, 32, 100), ("power", torch.bfloat16, 16, 90),
+                                             ("power", torch.bfloat16, 256, 150), ("power", torch.float32, 256, 80)])
 def test_fused_rope_matches_reference_rotation(kind, dtype, D, T):
     """poly_attention_hip(..., rope=(cos, sin)) on unrotated q/k against apply_rope + poly_attention_hip + autograd:
     output, dq, dk, dv (and dcoef / db) bit-identical. One q/k pair with head dims >= 32 applies the rotation's
-    gradient in the dQ / dK epilogues; two pairs and head dim 16 in a pass after the backward."""
+    gradient in the dQ / dK epilogues; two pairs, head dim 16 and fp32 at head dim 256 in a pass after the
+    backward."""
     from tensor_train_ing_amd import poly_attention_hip
     print(f"[rope fused] kind={kind} dtype={dtype} D={D} T={T}", flush=True)
     B, H = 2, 3

@@ -54,7 +54,7 @@ def _run(entry, kind, B, H, T, D, seed, rope=False):
 
 @pytest.mark.parametrize("kind,D,rope", [("offset_square", 64, False), ("lower_degree_mix", 64, False),
                                          ("offset_square", 128, False), ("power", 128, False), ("power", 128, True),
-                                         ("signed_product", 64, True)])
+                                         ("signed_product", 64, True), ("power", 256, True)])
 def test_noalloc_backward_equals_workspace_backward(kind, D, rope):
     print(f"[noalloc] kind={kind} D={D} rope={rope}", flush=True)
     for B, H, T, seed in ((2, 4, 700, 1), (1, 2, 190, 2)):  # the second call is smaller
