@@ -1,7 +1,7 @@
 """Benchmark: causal polynomial attention fwd+bwd TFLOP/s on one MI355X (BASELINE.json headline).
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--config 1b] [--kind power] [--dtype bf16]
-                    [--doc-len L] [--cpu-seconds S] [--no-cpu-baseline]
+                    [--doc-len L] [--head-dim D] [--rope] [--cpu-seconds S] [--no-cpu-baseline]
 
 A step is one forward + backward of the polynomial attention operator (default kind "power" at the config's
 degree; degree 2 equals the reference's signed_product with shared pairs) over one batch of seeded synthetic inputs
@@ -45,10 +45,10 @@ CONFIGS = {  # name: (B, H, T, D, degree, boost_rows, seed) -- BASELINE.json con
 }
 # matrix units (of 2*B*H*Npairs*D FLOP) each launch executes: fwd QK^T + PV; dv pass S + dV; dk pass S + dP + dK;
 # combined key side S + dP + dV + dK; dq pass S + dP + dQ; dQ from the stored dS tiles (qds) dQ only; with two
-# pairs one more S, dK and dQ each. The dO row-scaling pass and the dpar reduction are bandwidth kernels with no
-# matrix work.
-UNITS_ONE = {"fwd": 2, "dv": 2, "dk": 3, "kv": 4, "q": 3, "qds": 1, "scale": 0, "dpar": 0}
-UNITS_TWO = {"fwd": 3, "kv": 6, "q": 5, "qds": 2, "scale": 0, "dpar": 0}
+# pairs one more S, dK and dQ each (and one more S in the dv pass). The dO row-scaling pass, the dpar reduction and
+# the rotary pass are bandwidth kernels with no matrix work.
+UNITS_ONE = {"fwd": 2, "dv": 2, "dk": 3, "kv": 4, "q": 3, "qds": 1, "scale": 0, "dpar": 0, "rope": 0}
+UNITS_TWO = {"fwd": 3, "dv": 3, "dk": 5, "kv": 6, "q": 5, "qds": 2, "scale": 0, "dpar": 0, "rope": 0}
 
 
 def npairs(T, doc_len=0):
@@ -393,6 +393,9 @@ def main(argv=None):
                     help="q/k enter unrotated with rotary tables (positions within documents): the step includes the "
                          "one-pass rotation and the rotation's gradient inside the backward; also times the "
                          "reference's way (torch apply_rope, then the operator, autograd through both)")
+    ap.add_argument("--head-dim", type=int, default=0,
+                    help="run the config's B, H, T at this q/k and v head dim instead (16..256; a side line, not the "
+                         "headline)")
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--kernel-reps", type=int, default=50)
@@ -426,6 +429,7 @@ def main(argv=None):
         return bench_linear_ce(a)
     from tensor_train_ing_amd import poly_attention_hip
     B, H, T, D, degree, boost, seed = CONFIGS[a.config]
+    D = a.head_dim or D
     kind = a.kind
     two = kind in TWO_PAIR_KINDS
     tdt = torch.bfloat16 if a.dtype == "bf16" else torch.float32
@@ -497,7 +501,8 @@ def main(argv=None):
         "metric": METRIC, "value": round(value, 2), "unit": "TFLOP/s", "n_gpus": 1, "steps": a.steps,
         "warmup": a.warmup, "ms_per_step": round(ms, 4), "higher_is_better": True, "scaling": "weak",
         "vs_baseline": None, "dtype": a.dtype, "data": "synthetic",
-        "config": {"workload": f"polynomial attention fwd+bwd, BASELINE config '{a.config}': B{B} H{H} T{T} D{D} "
+        "config": {"workload": f"polynomial attention fwd+bwd, BASELINE config '{a.config}'"
+                               + (f" at head dim {D}" if a.head_dim else "") + f": B{B} H{H} T{T} D{D} "
                                + (f"degree {degree}" if kind == "power" else f"kind {kind}")
                                + f", causal{docs}, row scale (position in document + 1)^-1/2"
                                + (", rotary embedding of q/k inside the operator" if a.rope else ""),
@@ -513,11 +518,12 @@ def main(argv=None):
         "roofline": {"bound": "mfma", "kernel": dom, "achieved": round(ach, 2), "peak": peak,
                      "unit": "TFLOP/s", "frac": round(ach / peak, 4),
                      "traffic": (measured_traffic(a.config, dom)
-                                 if kind == "power" and not a.doc_len and a.dtype == "bf16" else None)},
+                                 if kind == "power" and not a.doc_len and a.dtype == "bf16" and not a.head_dim
+                                 else None)},
     }
     if rope_info is not None:
         line["rope"] = rope_info
-    if not a.no_cpu_baseline and kind == "power" and not a.doc_len and not a.rope:
+    if not a.no_cpu_baseline and kind == "power" and not a.doc_len and not a.rope and not a.head_dim:
         line["cpu_baseline"] = cpu_baseline(q, k, v, do, rs, degree, a.cpu_seconds)
     print(json.dumps(line), flush=True)
     return 0

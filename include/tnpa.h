@@ -29,7 +29,7 @@ extern "C" {
 typedef enum {
   TNPA_OK = 0,
   TNPA_ERR_INVALID = 1,     /* bad shape / stride / dtype / pointer: maps to Python ValueError */
-  TNPA_ERR_UNSUPPORTED = 2, /* valid per the reference contract but outside this build (e.g. head dim 256) */
+  TNPA_ERR_UNSUPPORTED = 2, /* valid per the reference contract but outside this build (e.g. head dim 512, fp32 with two q/k pairs above head dim 128) */
   TNPA_ERR_LAUNCH = 3       /* HIP launch failure: maps to Python RuntimeError */
 } tnpa_status;
 
