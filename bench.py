@@ -493,6 +493,8 @@ def main(argv=None):
     peak = PEAKS[a.dtype]
 
     units = UNITS_TWO if two else UNITS_ONE
+    if two and D > 128:  # the dk and q launches run once per pair, each with S1, S2 and dP
+        units = {**units, "dk": 8, "q": 8}
     dom = max(kt, key=lambda n: kt[n])
     ach = units[dom] * unit / (kt[dom] * 1e-3) / 1e12
     docs = f", documents of {a.doc_len} tokens" if a.doc_len else ", one document"

@@ -200,6 +200,9 @@ template <typename T, int POLY, int DK, int DV> struct Cfg {
   static constexpr int KV_NW = KV_SPLIT && !BIG ? NW2 : 4, KV_KW = 1;
   static constexpr int KV_BM = F32 || BIG || (NPAIR == 2 && DK > 64) ? 32 : 64;
   static constexpr int KV_WPE = SMALL ? 2 : 1, KV_SPLIT_WPE = BIG ? 1 : 2;
+  // two pairs above head dim 128: the dK pass and the dQ kernel run once per pair (both pairs' accumulators spilled
+  // ≈ 180 registers)
+  static constexpr bool PAIRSPLIT = BIG && NPAIR == 2;
   static constexpr int KV_KEYS = KV_NW * KV_KW * 32;
 };
 
@@ -634,7 +637,9 @@ k_fwd(const KParams p) {
 
 // ------------------------------------------------------------------------------------------------ dQ
 // ref: tnlm/kernels/poly_attn.py:151-202 (_bwd_q)
-template <typename T, int POLY, int DK, int DV, int NW, int QW, int BN, int WPE>
+// QSEL: -1 accumulates dQ of every q/k pair; 0 or 1 only that pair's (two-pair kinds above head dim 128, one launch
+// per pair: S1, S2 and dP are recomputed in each, and half the accumulators fit one wave's registers)
+template <typename T, int POLY, int DK, int DV, int NW, int QW, int BN, int WPE, int QSEL = -1>
 __global__ void __attribute__((amdgpu_flat_work_group_size(NW * 64, NW * 64), amdgpu_waves_per_eu(WPE)))
 k_bwd_q(const KParams p) {
   // four-wave workgroups at two waves per SIMD share a CU in pairs: each gets half of the 160 KB of LDS
@@ -733,13 +738,16 @@ k_bwd_q(const KParams p) {
     __syncthreads();
   }
 
-  f32x16 dq[NPAIR][QW][NDK];
+  // dQ accumulator sets: one per pair, or pair QSEL's alone (accumulator j holds pair qpair(j))
+  constexpr int NQA = QSEL < 0 ? NPAIR : 1;
+  auto qpair = [](int j) { return QSEL < 0 ? j : QSEL; };
+  f32x16 dq[NQA][QW][NDK];
 #pragma unroll
-  for (int pr = 0; pr < NPAIR; ++pr)
+  for (int j = 0; j < NQA; ++j)
 #pragma unroll
     for (int s = 0; s < QW; ++s)
 #pragma unroll
-      for (int d = 0; d < NDK; ++d) dq[pr][s][d] = zero16();
+      for (int d = 0; d < NDK; ++d) dq[j][s][d] = zero16();
 
   const int lo = (dst[m0] / BN) * BN;
   const int hi = min(m0 + BM, T_);
@@ -794,7 +802,7 @@ k_bwd_q(const KParams p) {
     mid();
     // H = row_scale * dO V^T before dS is formed and rounded, as ref: tnlm/kernels/poly_attn.py:188 does (keeps fp16
     // dS in range where the unscaled H times S would not be)
-    Op dso[NPAIR][QW][NC2];
+    Op dso[NQA][QW][NC2];
 #pragma unroll
     for (int s = 0; s < QW; ++s) {
       if (!(ALL || ((am >> s) & 1u))) continue;
@@ -816,20 +824,24 @@ k_bwd_q(const KParams p) {
       }
 #pragma unroll
       for (int c2 = 0; c2 < NC2; ++c2) {
-        dso[0][s][c2] = M::cvt(d1 + c2 * EPL);
-        if constexpr (NPAIR == 2) dso[NPAIR - 1][s][c2] = M::cvt(d2 + c2 * EPL);
+        if constexpr (QSEL < 0) {
+          dso[0][s][c2] = M::cvt(d1 + c2 * EPL);
+          if constexpr (NPAIR == 2) dso[NPAIR - 1][s][c2] = M::cvt(d2 + c2 * EPL);
+        } else {
+          dso[0][s][c2] = M::cvt((QSEL == 1 ? d2 : d1) + c2 * EPL);
+        }
       }
     }
 #pragma unroll
-    for (int pr = 0; pr < NPAIR; ++pr)
+    for (int j = 0; j < NQA; ++j)
 #pragma unroll
       for (int d = 0; d < NDK; ++d)
 #pragma unroll
         for (int c2 = 0; c2 < NC2; ++c2) {
-          const Op a = read_col<T, KTile>(base + pr * KTile::BYTES, 32 * kb + c2 * KC, 32 * d, lane);
+          const Op a = read_col<T, KTile>(base + qpair(j) * KTile::BYTES, 32 * kb + c2 * KC, 32 * d, lane);
 #pragma unroll
           for (int s = 0; s < QW; ++s)
-            if (ALL || ((am >> s) & 1u)) dq[pr][s][d] = M::mma(a, dso[pr][s][c2], dq[pr][s][d]);
+            if (ALL || ((am >> s) & 1u)) dq[j][s][d] = M::mma(a, dso[j][s][c2], dq[j][s][d]);
         }
   };
 
@@ -911,11 +923,12 @@ k_bwd_q(const KParams p) {
   // dQ rows: scaled by the chain-rule factor in registers, gathered in LDS, written as whole rows
   const TDesc* outs[2] = {&p.dq1, &p.dq2};
 #pragma unroll
-  for (int pr = 0; pr < NPAIR; ++pr) {
+  for (int j = 0; j < NQA; ++j) {
+    const int pr = qpair(j);
     __syncthreads();  // every wave is done with the tile buffers (or with the previous pair's rows)
 #pragma unroll
     for (int s = 0; s < QW; ++s)
-      acc_rows_to_lds<T, QTile, NDK>(smem, 32 * (wave * QW + s), l32, h, dq[pr][s], p.gf, DK);
+      acc_rows_to_lds<T, QTile, NDK>(smem, 32 * (wave * QW + s), l32, h, dq[j][s], p.gf, DK);
     __syncthreads();
     Stage<T, BM, DK, DKP, NT> os;
     if (p.rcos != nullptr)
@@ -931,7 +944,10 @@ k_bwd_q(const KParams p) {
 // MODE: KV_BOTH computes dK and dV in one pass (one wave per SIMD: dK, dV, K and V all stay in registers);
 // KV_DV and KV_DK split them into two passes that each fit two waves per SIMD (the S = Q K^T product is computed
 // in both passes).
-enum { KV_BOTH = 0, KV_DV = 1, KV_DK = 2 };
+// KV_DK1 / KV_DK2: the dK pass of a two-pair kind accumulating dK1 or dK2 only (above head dim 128, one launch per
+// pair: S1, S2 and dP are recomputed in each, and half the accumulators fit one wave's registers; the first writes
+// the dcoef/db partials).
+enum { KV_BOTH = 0, KV_DV = 1, KV_DK = 2, KV_DK1 = 3, KV_DK2 = 4 };
 template <typename T, int POLY, int DK, int DV, int NW, int KW, int BMQ, int WPE, int MODE>
 __global__ void __attribute__((amdgpu_flat_work_group_size(NW * 64, NW * 64), amdgpu_waves_per_eu(WPE)))
 k_bwd_kv(const KParams p) {
@@ -940,8 +956,11 @@ k_bwd_kv(const KParams p) {
   constexpr int KC = M::KC, EPL = M::EPL, NT = NW * 64;
   constexpr int NPAIR = two_pair_poly(POLY) ? 2 : 1;
   constexpr bool PRE = prescaled<T, POLY>();
-  constexpr bool PAR = (POLY == POLY_OS || POLY == POLY_GEN2) && MODE != KV_DV;  // kinds with head scalars
-  constexpr bool WANT_DV = MODE != KV_DK, WANT_DK = MODE != KV_DV;
+  constexpr bool PAR = (POLY == POLY_OS || POLY == POLY_GEN2) && MODE != KV_DV && MODE != KV_DK2;  // head scalars
+  constexpr bool WANT_DV = MODE == KV_BOTH || MODE == KV_DV, WANT_DK = MODE != KV_DV;
+  // dK accumulator sets: one per pair, or one pair's alone (accumulator j holds pair kpair(j))
+  constexpr int NDKA = MODE == KV_DK1 || MODE == KV_DK2 ? 1 : NPAIR;
+  auto kpair = [](int j) { return MODE == KV_DK2 ? 1 : j; };
   constexpr int DKP = DK < 32 ? 32 : DK, DVP = DV < 32 ? 32 : DV;
   constexpr int NCK = DK / KC, NCV = DV / KC, NDK = DKP / 32, NDV = DVP / 32, NQB = BMQ / 32, NC2 = 32 / KC;
   constexpr int BNK = NW * KW * 32;
@@ -1029,15 +1048,15 @@ k_bwd_kv(const KParams p) {
     __syncthreads();
   }
 
-  f32x16 dk[NPAIR][KW][NDK], dv[KW][NDV];
+  f32x16 dk[NDKA][KW][NDK], dv[KW][NDV];
 #pragma unroll
   for (int s = 0; s < KW; ++s) {
 #pragma unroll
     for (int d = 0; d < NDV; ++d) dv[s][d] = zero16();
 #pragma unroll
-    for (int pr = 0; pr < NPAIR; ++pr)
+    for (int j = 0; j < NDKA; ++j)
 #pragma unroll
-      for (int d = 0; d < NDK; ++d) dk[pr][s][d] = zero16();
+      for (int d = 0; d < NDK; ++d) dk[j][s][d] = zero16();
   }
   float gsum[4] = {0.f, 0.f, 0.f, 0.f};
 
@@ -1124,7 +1143,7 @@ k_bwd_kv(const KParams p) {
     }
     mid();
     Op po[KW][NC2];
-    Op dso[NPAIR][KW][NC2];
+    Op dso[NDKA][KW][NC2];
 #pragma unroll
     for (int s = 0; s < KW; ++s) {
       if (!(ALL || ((am >> s) & 1u))) continue;
@@ -1158,9 +1177,11 @@ k_bwd_kv(const KParams p) {
 #pragma unroll
       for (int c2 = 0; c2 < NC2; ++c2) {
         if constexpr (WANT_DV) po[s][c2] = M::cvt(pv + c2 * EPL);
-        if constexpr (WANT_DK) {
+        if constexpr (WANT_DK && NDKA == NPAIR) {
           dso[0][s][c2] = M::cvt(d1 + c2 * EPL);
           if constexpr (NPAIR == 2) dso[NPAIR - 1][s][c2] = M::cvt(d2 + c2 * EPL);
+        } else if constexpr (WANT_DK) {
+          dso[0][s][c2] = M::cvt((MODE == KV_DK2 ? d2 : d1) + c2 * EPL);
         }
       }
     }
@@ -1202,15 +1223,15 @@ k_bwd_kv(const KParams p) {
     if constexpr (DS_MID) store_ds();
     if constexpr (WANT_DK) {
 #pragma unroll
-      for (int pr = 0; pr < NPAIR; ++pr)
+      for (int j = 0; j < NDKA; ++j)
 #pragma unroll
         for (int d = 0; d < NDK; ++d)
 #pragma unroll
           for (int c2 = 0; c2 < NC2; ++c2) {
-            const Op a = read_col<T, QTile>(base + pr * QTile::BYTES, 32 * qb + c2 * KC, 32 * d, lane);
+            const Op a = read_col<T, QTile>(base + kpair(j) * QTile::BYTES, 32 * qb + c2 * KC, 32 * d, lane);
 #pragma unroll
             for (int s = 0; s < KW; ++s)
-              if (ALL || ((am >> s) & 1u)) dk[pr][s][d] = M::mma(a, dso[pr][s][c2], dk[pr][s][d]);
+              if (ALL || ((am >> s) & 1u)) dk[j][s][d] = M::mma(a, dso[j][s][c2], dk[j][s][d]);
           }
     }
     if constexpr (!DS_MID) store_ds();
@@ -1317,10 +1338,11 @@ k_bwd_kv(const KParams p) {
     }
     if constexpr (WANT_DK) {
 #pragma unroll
-      for (int pr = 0; pr < NPAIR; ++pr) {
+      for (int j = 0; j < NDKA; ++j) {
+        const int pr = kpair(j);
         __syncthreads();  // every wave is done with the tile buffers (or with the previous rows)
 #pragma unroll
-        for (int s = 0; s < KW; ++s) acc_rows_to_lds<T, KRows, NDK>(smem, 32 * (wave * KW + s), l32, h, dk[pr][s], p.gf, DK);
+        for (int s = 0; s < KW; ++s) acc_rows_to_lds<T, KRows, NDK>(smem, 32 * (wave * KW + s), l32, h, dk[j][s], p.gf, DK);
         __syncthreads();
         Stage<T, BNK, DK, DKP, NT> os;
         if (p.rcos != nullptr)
@@ -1346,7 +1368,8 @@ k_bwd_kv(const KParams p) {
                       dv[s][d][4 * g + 3] * p.vf);
         }
 #pragma unroll
-      for (int pr = 0; pr < (WANT_DK ? NPAIR : 0); ++pr) {
+      for (int j = 0; j < (WANT_DK ? NDKA : 0); ++j) {
+        const int pr = kpair(j);
         T* krow = head_ptr_w<T>(*kouts[pr], b, hd) + (int64_t)key * kouts[pr]->st;
 #pragma unroll
         for (int d = 0; d < NDK; ++d)
@@ -1354,8 +1377,8 @@ k_bwd_kv(const KParams p) {
           for (int g = 0; g < 4; ++g) {
             const int col = 32 * d + 8 * g + 4 * h;
             if (col < DK)
-              store4<T>(krow + col, dk[pr][s][d][4 * g] * p.gf, dk[pr][s][d][4 * g + 1] * p.gf,
-                        dk[pr][s][d][4 * g + 2] * p.gf, dk[pr][s][d][4 * g + 3] * p.gf);
+              store4<T>(krow + col, dk[j][s][d][4 * g] * p.gf, dk[j][s][d][4 * g + 1] * p.gf,
+                        dk[j][s][d][4 * g + 2] * p.gf, dk[j][s][d][4 * g + 3] * p.gf);
           }
       }
     }
@@ -1872,9 +1895,17 @@ template <typename T, int POLY, int DK, int DV> hipError_t launch_bwd_kv(const K
     if (p.kvsel & 1)
       hipLaunchKernelGGL((k_bwd_kv<T, POLY, DK, DV, C::KV_NW, C::KV_KW, C::KV_BM, C::KV_SPLIT_WPE, KV_DV>), dim3(grid),
                          dim3(C::KV_NW * 64), 0, st, p);
-    if (p.kvsel & 2)
-      hipLaunchKernelGGL((k_bwd_kv<T, POLY, DK, DV, C::KV_NW, C::KV_KW, C::KV_BM, C::KV_SPLIT_WPE, KV_DK>), dim3(grid),
-                         dim3(C::KV_NW * 64), 0, st, p);
+    if (p.kvsel & 2) {
+      if constexpr (C::PAIRSPLIT) {
+        hipLaunchKernelGGL((k_bwd_kv<T, POLY, DK, DV, C::KV_NW, C::KV_KW, C::KV_BM, C::KV_SPLIT_WPE, KV_DK1>),
+                           dim3(grid), dim3(C::KV_NW * 64), 0, st, p);
+        hipLaunchKernelGGL((k_bwd_kv<T, POLY, DK, DV, C::KV_NW, C::KV_KW, C::KV_BM, C::KV_SPLIT_WPE, KV_DK2>),
+                           dim3(grid), dim3(C::KV_NW * 64), 0, st, p);
+      } else {
+        hipLaunchKernelGGL((k_bwd_kv<T, POLY, DK, DV, C::KV_NW, C::KV_KW, C::KV_BM, C::KV_SPLIT_WPE, KV_DK>),
+                           dim3(grid), dim3(C::KV_NW * 64), 0, st, p);
+      }
+    }
   } else {
     hipLaunchKernelGGL((k_bwd_kv<T, POLY, DK, DV, C::KV_NW, C::KV_KW, C::KV_BM, C::KV_WPE, KV_BOTH>), dim3(grid),
                        dim3(C::KV_NW * 64), 0, st, p);
@@ -1889,8 +1920,15 @@ template <typename T, int POLY, int DK, int DV> hipError_t launch_bwd_q(const KP
   typedef Cfg<T, POLY, DK, DV> C;
   constexpr int BM = C::BQ_NW * C::BQ_QW * 32;
   const int grid = p.B * p.H * ((p.T + BM - 1) / BM);
-  hipLaunchKernelGGL((k_bwd_q<T, POLY, DK, DV, C::BQ_NW, C::BQ_QW, C::BQ_BN, C::BQ_WPE>), dim3(grid), dim3(C::BQ_NW * 64), 0, st,
-                     p);
+  if constexpr (C::PAIRSPLIT) {
+    hipLaunchKernelGGL((k_bwd_q<T, POLY, DK, DV, C::BQ_NW, C::BQ_QW, C::BQ_BN, C::BQ_WPE, 0>), dim3(grid),
+                       dim3(C::BQ_NW * 64), 0, st, p);
+    hipLaunchKernelGGL((k_bwd_q<T, POLY, DK, DV, C::BQ_NW, C::BQ_QW, C::BQ_BN, C::BQ_WPE, 1>), dim3(grid),
+                       dim3(C::BQ_NW * 64), 0, st, p);
+  } else {
+    hipLaunchKernelGGL((k_bwd_q<T, POLY, DK, DV, C::BQ_NW, C::BQ_QW, C::BQ_BN, C::BQ_WPE>), dim3(grid),
+                       dim3(C::BQ_NW * 64), 0, st, p);
+  }
   return hipGetLastError();
   }
 }
