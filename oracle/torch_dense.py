@@ -3,7 +3,7 @@
 The same dense form as oracle/poly_attention.py -- ref: tnlm/attention.py:54-77: S = q k^T / sqrt(dk), A = A(S1, S2)
 (ref: tnlm/kernels/poly_attn.py:26-34, plus the degree-p power), P = C * A with C = visible * row scale applied
 after the polynomial, y = P v -- restated with torch tensor ops so that `bench.py` can time it in float32 on the
-host's cores with autograd providing the backward, as BASELINE.md's CPU plan asks. It is pinned against the numpy
+host's cores with autograd providing the backward (a float32 torch CPU baseline). It is pinned against the numpy
 oracle in tests/test_oracle.py. Nothing in the product package imports it.
 """
 from __future__ import annotations

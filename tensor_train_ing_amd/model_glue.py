@@ -3,8 +3,8 @@
 The reference model prepares its fast path in `make_ctx` (ref: tnlm/model.py:205-227): with a fast backend it builds
 no T x T mask, only the per-query row scales n_visible^-p (n_visible = position in document + 1, 0 for padding;
 ref: tnlm/model.py:217-221), and `Attention.forward` hands them to the operator (ref: tnlm/model.py:86-91). These
-functions do the same for "hip", so the reference's model code needs only its backend test widened
-(INTEGRATION.md shows the patch). `source_sha256` extends the checkpoint's source identity
+functions do the same for "hip", so the reference's model code needs only its backend test widened to accept
+"hip". `source_sha256` extends the checkpoint's source identity
 (ref: tnlm/checkpoint.py:54) with this package's kernel sources.
 """
 from __future__ import annotations

@@ -1,6 +1,6 @@
 """CPU checks of the C ABI (include/tnpa.h) and the host-side operator logic; no GPU compute is launched.
 
-Failure handling the survey asks to force on the CPU: malformed shapes/strides/dtypes/head dims return an error code
+Failure handling forced on the CPU: malformed shapes/strides/dtypes/head dims return an error code
 and message before anything is enqueued; a differentiable row_scale is rejected; a missing library fails loudly.
 """
 from __future__ import annotations
