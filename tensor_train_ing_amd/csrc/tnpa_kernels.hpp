@@ -196,10 +196,13 @@ template <typename T, int POLY, int DK, int DV> struct Cfg {
   // would need 376 registers there); up to 64 the combined kernel fits 256 registers and saves the S recompute.
   static constexpr bool KV_SPLIT = (TWO && !SMALL) || BIG;
   // (two pairs at head dim 128: 32-query tiles, whose operand reads the compiler keeps in flight fit the one-wave
-  // kernel's 512 registers without spills; 64-query tiles spilled 13 registers and ran 20% slower)
+  // kernel's 512 registers without spills; 64-query tiles spilled 13 registers and ran 20% slower. Two pairs up to
+  // head dim 64: 32-query tiles at two waves per SIMD, two 28 KB workgroups per CU (41-76 registers spilled),
+  // same-process A/B at the 100m shape: key side lower_degree_mix 0.257 -> 0.238 ms, signed_product 0.150 -> 0.149;
+  // the 32-query tiles at one wave per SIMD alone were slower, 0.275 / 0.164)
   static constexpr int KV_NW = KV_SPLIT && !BIG ? NW2 : 4, KV_KW = 1;
-  static constexpr int KV_BM = F32 || BIG || (NPAIR == 2 && DK > 64) ? 32 : 64;
-  static constexpr int KV_WPE = SMALL ? 2 : 1, KV_SPLIT_WPE = BIG ? 1 : 2;
+  static constexpr int KV_BM = F32 || BIG || NPAIR == 2 ? 32 : 64;
+  static constexpr int KV_WPE = SMALL || PAIR2_TWO ? 2 : 1, KV_SPLIT_WPE = BIG ? 1 : 2;
   // two pairs above head dim 128: the dK pass and the dQ kernel run once per pair (both pairs' accumulators spilled
   // ≈ 180 registers)
   static constexpr bool PAIRSPLIT = BIG && NPAIR == 2;
