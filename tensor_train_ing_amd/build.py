@@ -33,12 +33,14 @@ HEADERS = ("tnpa_device.hpp", "tnpa_kernels.hpp", "tnpa_params.hpp", "tnpa_inter
 
 
 def _units():
-    units = [("tnpa_api", CSRC / "tnpa_api.hip", []), ("tnce", CSRC / "tnce.hip", [])]
-    for tag, ctype in ELEMENT_TYPES.items():
-        for dk in HEAD_DIMS:
+    """Translation units, longest compiles first (larger head dims, fp32 first; 40-140 s each) so the parallel
+    build's last unit to start is a short one."""
+    units = []
+    for dk in sorted(HEAD_DIMS, reverse=True):
+        for tag in ("f32", "bf16", "f16"):
             units.append((f"tnpa_inst_{tag}_dk{dk}", CSRC / "tnpa_inst.hip",
-                          [f"-DTNPA_INST_T={ctype}", f"-DTNPA_INST_DK={dk}"]))
-    return units
+                          [f"-DTNPA_INST_T={ELEMENT_TYPES[tag]}", f"-DTNPA_INST_DK={dk}"]))
+    return units + [("tnpa_api", CSRC / "tnpa_api.hip", []), ("tnce", CSRC / "tnce.hip", [])]
 
 
 def _stale(obj: Path, src: Path) -> bool:
