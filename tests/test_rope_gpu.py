@@ -57,7 +57,9 @@ def test_rope_kernel_matches_reference_apply_rope(dtype, D, layout):
                                              ("signed_product", torch.bfloat16, 128, 250),
                                              ("lower_degree_mix", torch.bfloat16, 64, 130),
                                              ("power", torch.float32, 32, 100), ("power", torch.bfloat16, 16, 90),
-                                             ("power", torch.bfloat16, 256, 150), ("power", torch.float32, 256, 80)])
+                                             ("power", torch.bfloat16, 256, 150), ("power", torch.float32, 256, 80),
+                                             ("signed_product", torch.bfloat16, 256, 120),
+                                             ("lower_degree_mix", torch.float16, 256, 100)])
 def test_fused_rope_matches_reference_rotation(kind, dtype, D, T):
     """poly_attention_hip(..., rope=(cos, sin)) on unrotated q/k against apply_rope + poly_attention_hip + autograd:
     output, dq, dk, dv (and dcoef / db) bit-identical. One q/k pair with head dims >= 32 applies the rotation's
