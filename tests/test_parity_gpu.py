@@ -637,7 +637,9 @@ def test_doc_bounds_match_oracle(T, dtype):
 @pytest.mark.parametrize("kind,B,H,T,D,dtype", [
     ("power", 2, 3, 300, 128, torch.bfloat16), ("power", 1, 2, 1000, 64, torch.bfloat16),
     ("signed_product", 2, 2, 260, 128, torch.bfloat16), ("lower_degree_mix", 1, 3, 200, 64, torch.float16),
-    ("offset_square", 2, 2, 150, 32, torch.float32), ("signed_product", 1, 2, 77, 16, torch.float32)])
+    ("offset_square", 2, 2, 150, 32, torch.float32), ("signed_product", 1, 2, 77, 16, torch.float32),
+    ("power", 1, 2, 200, 256, torch.bfloat16), ("signed_product", 1, 2, 150, 256, torch.bfloat16),
+    ("power", 1, 2, 90, 256, torch.float32)])
 def test_forward_score_norms_equal_the_reference_bound(kind, B, H, T, D, dtype):
     """The forward kernel's per-head max |q| and max |k| (every token, padding included) equal the reference's
     score_bound factors q.float().norm(-1).amax((0, 2)) (ref: tnlm/model.py:33-38) to float32 rounding, with
